@@ -1,0 +1,266 @@
+"""Benchmark: hierarchical-attention forward on one MI355X.
+
+Workload ("Wan2.2-5B-shaped layer"): 4 players x 42 latent
+frames x 220 tokens, groups {0,1},{2,3} fixed, K_L=5 local and K_G=6 global hub
+tokens per frame, n=3 frames per causal block, window W=21, 24 heads x 128,
+bf16, q/k/v ~ 0.5 N(0,1) (synthetic).  One "step" is one full-sequence forward
+of the hierarchical attention of one layer: all 14 temporal blocks in one
+launch, Q/K/V already resident in HBM.  Metadata (topology build) is built
+once before timing, like the reference's cached layouts; its device latency is
+reported separately, as is the fused Q/K prologue.
+
+Prints one JSON line (the driver contract).  ``--config c3|c4|...`` runs the
+other player counts for the DESIGN tables instead.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 (256 CU x 2.4 GHz x 4096 FLOP/clk)
+SEED = 20260813
+
+CONFIGS = {
+    # name: (P, T, L, N, KL, KG, n, W, H, D, grouping)
+    "c2": (4, 42, 220, 2, 5, 6, 3, 21, 24, 128, "fixed"),
+    "c2_w7": (4, 42, 220, 2, 5, 6, 3, 7, 24, 128, "fixed"),
+    "p6": (6, 42, 220, 3, 5, 6, 3, 21, 24, 128, "pairs"),
+    "c3": (8, 42, 220, 3, 5, 6, 3, 21, 24, 128, "dynamic"),
+    "p10": (10, 42, 220, 4, 5, 6, 3, 21, 24, 128, "random_block"),
+}
+
+
+def grouping(name, P, T, N, rng):
+    """Synthetic topologies; returns (labels or None, membership or None, global_only or None)."""
+    if name == "fixed":
+        labels = np.array([[p // 2 for p in range(P)]] * T)
+        return labels, None, None
+    if name == "pairs":
+        labels = np.array([[min(p // 2, N - 1) for p in range(P)]] * T)
+        return labels, None, None
+    if name == "dynamic":
+        # 2D random walk, distance threshold 0.3, components of size >= 2 take
+        # slots by (-size, min id); the rest are global-only.  Recomputed per frame.
+        pos = rng.random((P, 2))
+        mem = np.zeros((T, N, P), dtype=bool)
+        go = np.zeros((T, P), dtype=bool)
+        for t in range(T):
+            pos = np.clip(pos + rng.normal(0, 0.05, pos.shape), 0, 1)
+            d = np.linalg.norm(pos[:, None] - pos[None], axis=-1) < 0.3
+            comp = -np.ones(P, dtype=int)
+            c = 0
+            for p in range(P):
+                if comp[p] >= 0:
+                    continue
+                stack = [p]
+                comp[p] = c
+                while stack:
+                    x = stack.pop()
+                    for y in np.nonzero(d[x])[0]:
+                        if comp[y] < 0:
+                            comp[y] = c
+                            stack.append(y)
+                c += 1
+            groups = [np.nonzero(comp == i)[0] for i in range(c)]
+            groups = sorted([g for g in groups if len(g) >= 2], key=lambda g: (-len(g), g.min()))
+            for slot, g in enumerate(groups[:N]):
+                mem[t, slot, g] = True
+            go[t] = ~mem[t].any(0)
+        return None, mem, go
+    if name == "random_block":
+        mem = np.zeros((T, N, P), dtype=bool)
+        for b in range(0, T, 3):
+            g = rng.integers(3, N + 1)
+            assign = rng.integers(0, g, size=P)
+            for t in range(b, min(b + 3, T)):
+                mem[t, assign, np.arange(P)] = True
+        go = ~mem.any(1)
+        return None, mem, go
+    raise ValueError(name)
+
+
+def build_case(cfg, device):
+    from multics_amd import metadata as M
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS[cfg]
+    rng = np.random.default_rng(SEED)
+    labels, mem, go = grouping(grp, P, T, N, rng)
+    topo = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W, direct=True,
+                                    labels=labels, membership=mem, global_only=go)
+    t0 = time.perf_counter()
+    res = M.build(topo, device)
+    torch.cuda.synchronize()
+    host_build_s = time.perf_counter() - t0
+    return topo, res.tiles, host_build_s, (labels, mem, go)
+
+
+def time_events(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(steps):
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+    return times
+
+
+def cpu_baseline(cfg, topo_args, budget_s=20.0):
+    """The oracle's masked-SDPA restatement (dense bool mask + fp32 SDPA) on a
+    bounded sample of (temporal block, head) pairs, extrapolated to the layer."""
+    from oracle.masks import FullTopology, mask_rows
+    P, T, L, N, KL, KG, n, W, H, D, _ = CONFIGS[cfg]
+    labels, mem, go = topo_args
+    ft = FullTopology(P, T, L, N, KL, KG, n, W, True, labels=labels, membership=mem, global_only=go)
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    S = ft.S
+    g = torch.Generator().manual_seed(SEED)
+    b = min(7, T // n - 1)                       # a steady-state block
+    frames = range(b * n, b * n + n)
+    local_start, global_start = P * T * L, P * T * L + T * N * KL
+    rows = [(p * T + f) * L + i for p in range(P) for f in frames for i in range(L)]
+    rows += [local_start + (f * N + gg) * KL + i for f in frames for gg in range(N) for i in range(KL)]
+    rows += [global_start + f * KG + i for f in frames for i in range(KG)]
+    rows = np.array(rows)
+    mask = torch.zeros(len(rows), S, dtype=torch.bool)
+    for r0 in range(0, len(rows), 256):
+        mask[r0:r0 + 256] = torch.from_numpy(mask_rows(ft, q_idx=rows[r0:r0 + 256]))
+    q = torch.randn(1, 1, len(rows), D, generator=g) * 0.5
+    k = torch.randn(1, 1, S, D, generator=g) * 0.5
+    v = torch.randn(1, 1, S, D, generator=g) * 0.5
+    done, t_sum = 0, 0.0
+    while done < H and (done == 0 or t_sum < budget_s):
+        t0 = time.perf_counter()
+        torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask[None, None])
+        t_sum += time.perf_counter() - t0
+        done += 1
+    per_block_head = t_sum / done
+    ms_layer = per_block_head * (T // n) * H * 1e3
+    return dict(ms_layer=ms_layer, sample=f"{done} head(s) of temporal block {b} of {T // n} "
+                f"({len(rows)} query rows x {S} keys, dense mask SDPA fp32), extrapolated x"
+                f"{(T // n) * H / done:.0f}", cores=cores, threads=torch.get_num_threads(),
+                cpu=platform.processor() or platform.machine())
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the hierarchical attention of one layer shards by "
+              "head or temporal block with no exchange inside the kernel; "
+              "multi-GPU runs are not part of this build.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from multics_amd.kernels import hier_attention_forward, qkv_prologue
+    dev = torch.device("cuda", 0)
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS[args.config]
+    topo, tiles, host_build_s, topo_args = build_case(args.config, dev)
+    S = P * T * L + T * (N * KL + KG)
+
+    # metadata builder latency (device passes + the count readback)
+    from multics_amd import metadata as M
+    meta_ms = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        M.build(topo, dev)
+        torch.cuda.synchronize()
+        meta_ms.append((time.perf_counter() - t0) * 1e3)
+
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    mk = lambda: (torch.randn(H, S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    qh, kh, vh = mk(), mk(), mk()
+    q, k, v = (t.permute(1, 0, 2) for t in (qh, kh, vh))       # [S,H,D] views, head-major storage
+    out = torch.empty(S, H, D, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        hier_attention_forward(q, k, v, tiles, out)
+
+    times = time_events(step, args.steps, args.warmup)
+    ms = float(np.median(times))
+    ms_mean = float(np.mean(times))
+    useful_flop = 4.0 * H * D * tiles.logical_pairs
+    tflops = useful_flop / (ms * 1e-3) / 1e12
+
+    # fused Q/K prologue (camera + RMSNorm + RoPE) on the same sequence
+    dim = H * D
+    qx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
+    kx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
+    vx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
+    cam = torch.zeros(S, 12, device=dev, dtype=torch.bfloat16)
+    cam[:P * T * L] = torch.randn(P * T * L, 12, generator=g, device=dev).to(torch.bfloat16)
+    wcq = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
+    wck = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
+    nw = torch.ones(dim, dtype=torch.bfloat16, device=dev)
+    ang = torch.rand(S, D // 2, generator=g, device=dev) * 6.28
+    cs, sn = torch.cos(ang), torch.sin(ang)
+    pro = time_events(lambda: qkv_prologue(qx, kx, vx, norm_q_w=nw, norm_k_w=nw, rope_cos=cs,
+                                           rope_sin=sn, num_heads=H, eps=1e-6, cam=cam,
+                                           w_cam_q=wcq, w_cam_k=wck, out_layout="hsd"),
+                      max(args.steps // 5, 3), 2)
+    pro_ms = float(np.median(pro))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(args.config, topo_args, args.cpu_budget)
+        cpu = {"value": round(useful_flop / (cb["ms_layer"] * 1e-3) / 1e12, 6),
+               "unit": "TFLOP/s (useful)", "ms_per_layer": round(cb["ms_layer"], 1),
+               "cores": cb["cores"], "threads": cb["threads"], "kind": "port",
+               "cpu": cb["cpu"], "sample": cb["sample"]}
+
+    line = {
+        "metric": "hier-attn useful TFLOP/s + ms/layer fwd (bf16, 4 and 10 players, 1 GPU)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "ms_per_step_mean": round(ms_mean, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (q/k/v ~ 0.5 N(0,1), seeded)",
+        "config": {"workload": f"{args.config}: full-sequence hierarchical attention fwd, P={P} "
+                   f"T={T} L={L} N={N} K_L={KL} K_G={KG} n={n} W={W} H={H} D={D} ({grp} groups)",
+                   "players": P, "tokens": S, "useful_pairs": tiles.logical_pairs,
+                   "useful_gflop": round(useful_flop / 1e9, 1), "seed": SEED},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": {"metadata_build_ms": round(float(np.median(meta_ms)), 3),
+                  "prologue_ms": round(pro_ms, 4), "work_items": tiles.n_items * H},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,198 @@
+/*
+ * hierattn.h -- C ABI of the MI355X (gfx950) hierarchical group attention.
+ *
+ * Plain C: no HIP, torch or C++ types in any signature.  Every pointer named
+ * "device" is a HIP device pointer owned by the caller; the library never
+ * allocates or frees caller memory.  Every call is asynchronous on the given
+ * stream (a hipStream_t passed as void*, NULL = the null stream) and returns
+ * 0 on success or a negative HIER_E* code; hier_last_error() then returns a
+ * thread-local message.
+ *
+ * Token orders used below (reference definitions):
+ *   full sequence  [P*T*L agents p-major | T*N*KL locals time-major | T*KG global]
+ *                  multics/models/hier_masks.py:549-571
+ *   cached pool    [P*fa*L agents p-major | N*fl*KL locals g-major | fg*KG global]
+ *                  multics/models/kernels/hier_segmented_attention.py:247-258
+ *   cached queries [P*n*L agents | n*N*KL locals | n*KG global]
+ *                  multics/models/attention.py:474-476
+ */
+#ifndef HIERATTN_H
+#define HIERATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  HIER_OK = 0,
+  HIER_EINVAL = -1,      /* invalid argument        -> ValueError          */
+  HIER_EUNSUPPORTED = -2,/* unsupported shape/dtype -> NotImplementedError */
+  HIER_ELAUNCH = -3,     /* HIP launch/runtime error -> RuntimeError       */
+  HIER_EINTERNAL = -4    /* violated internal invariant -> AssertionError  */
+};
+
+/* ------------------------------------------------------------------------ */
+/* Topology of B independent temporal blocks (one cached call is B = 1; a    */
+/* full-sequence forward is B = T / n).  All arrays are DEVICE pointers.     */
+/* ------------------------------------------------------------------------ */
+typedef struct HierTopo {
+  int32_t P, N, L, KL, KG;          /* players, group slots, tokens per frame  */
+  int32_t n_frames, n_block;        /* query frames per block, causal block n  */
+  int32_t local_attn;               /* sliding window W in frames, -1 = none   */
+  int32_t direct;                   /* same-group, same-block player edges     */
+  int32_t no_local;                 /* K_L = 0 topology (hier_no_local_hub)    */
+  int32_t use_membership;           /* membership/global_only (else labels)    */
+  int32_t B;                        /* number of blocks                        */
+  int32_t fa_max, fl_max, fg_max;   /* row pitch of the per-block frame arrays */
+  int32_t T_mem;                    /* rows of membership / global_only        */
+  /* per block */
+  const int32_t* fa;                /* [B] agent frames per player stream      */
+  const int32_t* fl;                /* [B] frames per local stream             */
+  const int32_t* fg;                /* [B] global frames                       */
+  const int32_t* agent_frames;      /* [B][P][fa_max] absolute frame ids, ascending */
+  const int32_t* local_frames;      /* [B][N][fl_max]                          */
+  const int32_t* global_frames;     /* [B][fg_max]                             */
+  const uint8_t* local_active;      /* [B][N][fl_max] local slot active per cached frame */
+  const int32_t* q_frames;          /* [B][n_frames] absolute query frames     */
+  const int32_t* labels;            /* [B][n_frames][P] (labels mode)          */
+  const uint8_t* q_active;          /* [B][n_frames][N]                        */
+  const uint8_t* membership;        /* [T_mem][N][P] (membership mode)         */
+  const uint8_t* global_only;       /* [T_mem][P]                              */
+  /* addressing: token offset of frame fi of each stream, for the reference  */
+  /* arrays (ref_*) and for the attention kernel's K/V pool (tile_*)         */
+  const int32_t* ref_agent_base;    /* [B][P][fa_max]                          */
+  const int32_t* ref_local_base;    /* [B][N][fl_max]                          */
+  const int32_t* ref_global_base;   /* [B][fg_max]                             */
+  const int32_t* tile_agent_base;   /* [B][P][fa_max]                          */
+  const int32_t* tile_local_base;   /* [B][N][fl_max]                          */
+  const int32_t* tile_global_base;  /* [B][fg_max]                             */
+  /* query rows: first row and frame pitch of every stream (P + N + 1 per    */
+  /* block; local entries unused when no_local)                              */
+  const int32_t* ref_qbase;         /* [B][P+N+1]                              */
+  const int32_t* tile_qbase;        /* [B][P+N+1]                              */
+  int32_t ref_qstride[3];           /* frame pitch of agent / local / global rows */
+  int32_t tile_qstride[3];
+} HierTopo;
+
+/* Per-segment counts written by hier_meta_count (DEVICE arrays).           */
+/* Segment order inside a block follows _build_metadata:                    */
+/* players (p, qrel), locals (qrel, g), global (qrel).                       */
+typedef struct HierMetaCounts {
+  int32_t* seg_count;      /* [B][n_seg] compact key count per segment        */
+  int32_t* tiled_count;    /* [B][n_seg] kept Tiled128 slots (multiple of 128)*/
+  int32_t* dense_count;    /* [B][n_seg] dense slots                          */
+  int32_t* logical_count;  /* [B][n_seg] valid dense slots                    */
+  int32_t* tile_count;     /* [B][P+N+1] union keys per stream, padded to 64  */
+} HierMetaCounts;
+
+/* Output arrays written by hier_meta_build.  Any group may be NULL to skip. */
+typedef struct HierMetaOut {
+  /* _build_metadata format (bit-exact), block b at offsets *_off[b]         */
+  int32_t block_m;
+  const int64_t* seg_prog_off;    /* [B] program offset of block b            */
+  const int64_t* seg_kv_off;      /* [B] element offset of block b's matrix   */
+  const int32_t* seg_max_k;       /* [B] MAX_K of block b                      */
+  int32_t* seg_prog_qbase;        /* [sum programs]                            */
+  int32_t* seg_prog_nq;
+  int32_t* seg_prog_seg;
+  int32_t* seg_kv_index;          /* [sum n_seg*MAX_K]                         */
+  int32_t* seg_kv_count;          /* [B*n_seg]                                 */
+  /* Tiled128 format (labels only, bit-exact)                                */
+  const int64_t* tiled_prog_off;
+  const int64_t* tiled_kv_off;
+  const int32_t* tiled_max_k;
+  int32_t* tiled_prog_qbase;
+  int32_t* tiled_prog_nq;
+  int32_t* tiled_prog_seg;
+  int32_t* tiled_kv_index;
+  uint8_t* tiled_kv_valid;
+  int32_t* tiled_kv_count;
+  /* attention-kernel tile list: per (block, stream) the ordered union of its */
+  /* query frames' key lists with a per-key bitmask over query frames         */
+  const int64_t* tile_kv_off;     /* [B][P+N+1] key offset of each stream     */
+  const int32_t* tile_item_off;   /* [B][P+N+1] first work item of each stream */
+  int32_t rows_per_item;          /* query rows per work item (multiple of 32) */
+  int32_t* tile_kv_idx;           /* [sum tile_count] K/V pool token index     */
+  uint32_t* tile_kv_mask;         /* [sum tile_count] visible-to-query-frame bits */
+  uint32_t* tile_blk_and;         /* [sum tile_count / 64] AND of masks per 64 keys */
+  int32_t* tile_items;            /* [n_items][8] work item descriptors        */
+} HierMetaOut;
+
+/* Pass 1: evaluate the hierarchical edge rule for every (segment, cached   */
+/* frame run) and count.  Replaces the count half of _build_metadata         */
+/* (multics/models/kernels/hier_segmented_attention.py:156-395), _pack_layout */
+/* (hier_tiled_attention.py:182-241) and the cached/full-sequence Tiled128   */
+/* builders (hier_tiled_attention.py:244-429, 474-655).                      */
+int hier_meta_count(const HierTopo* topo, const HierMetaCounts* counts, void* stream);
+
+/* Pass 2: fill the arrays sized from pass 1's counts (same references).     */
+int hier_meta_build(const HierTopo* topo, const HierMetaOut* out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Q/K/V layout prologue: camera-pose Q/K adapter, RMSNorm over all heads,  */
+/* gain and RoPE fused into one pass that writes the attention layout.       */
+/* Replaces SelfAttention._project_self_attn_qkv after the three GEMMs      */
+/* (multics/models/attention.py:355-365, 307-320, 231-242) and rope_apply    */
+/* (multics/models/rope.py:248-254).                                         */
+/* ------------------------------------------------------------------------ */
+typedef struct HierPrologueArgs {
+  int32_t S, H, D;                 /* tokens, heads, head dim (D = 128)       */
+  float eps;                       /* RMSNorm epsilon                          */
+  const uint16_t* qx;              /* [S][H*D] bf16 q(x) (with bias)           */
+  const uint16_t* kx;              /* [S][H*D] bf16 k(x)                       */
+  const uint16_t* vx;              /* [S][H*D] bf16 v(x), copied to the layout */
+  const uint16_t* cam;             /* [S][C] bf16 camera tokens or NULL        */
+  const uint16_t* w_cam_q;         /* [H*D][C] bf16 cam_q.weight or NULL       */
+  const uint16_t* w_cam_k;         /* [H*D][C] bf16                            */
+  int32_t C;                       /* camera feature width (12)                */
+  const uint16_t* norm_q_w;        /* [H*D] bf16 RMSNorm gains                 */
+  const uint16_t* norm_k_w;
+  const float* rope_cos;           /* [S][D/2] fp32 (from the complex freqs)   */
+  const float* rope_sin;           /* [S][D/2]                                 */
+  uint16_t* q_out;                 /* bf16 outputs at [s*stride_s + h*stride_h + d] */
+  uint16_t* k_out;
+  uint16_t* v_out;
+  int64_t out_stride_s, out_stride_h;
+} HierPrologueArgs;
+
+int hier_qkv_prologue(const HierPrologueArgs* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Block-sparse frame-causal flash attention forward over the tile list.    */
+/* Replaces _segmented_attn_fwd / _tiled128_fwd launches                     */
+/* (hier_segmented_attention.py:27-114, 474-500; hier_tiled_attention.py:52-146, */
+/* 766-795) and the FlashInfer / varlen calls (hier_paged_attention.py:238-267, */
+/* hier_packed_attention.py:230-242).  Rows with no visible key are 0.       */
+/* ------------------------------------------------------------------------ */
+typedef struct HierFwdArgs {
+  int32_t H, D;                    /* heads, head dim (must be 128)            */
+  int32_t n_items;                 /* work items (tile_items rows)             */
+  float scale;                     /* softmax scale (1/sqrt(D))                */
+  const uint16_t* q;               /* bf16, element (s,h,d) at s*q_ss + h*q_sh + d */
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;                     /* bf16 output, rows not covered are untouched */
+  float* lse;                      /* [H][S_q] log-sum-exp (natural log) or NULL */
+  int64_t q_ss, q_sh, k_ss, k_sh, v_ss, v_sh, o_ss, o_sh;
+  int64_t lse_stride_h;            /* elements between heads of lse            */
+  const int32_t* tile_items;       /* from hier_meta_build                      */
+  const int32_t* tile_kv_idx;
+  const uint32_t* tile_kv_mask;
+  const uint32_t* tile_blk_and;
+} HierFwdArgs;
+
+int hier_attn_fwd(const HierFwdArgs* args, void* stream);
+
+/* Last error message of the calling thread ("" if none).                    */
+const char* hier_last_error(void);
+
+/* Library version string and the offload target it was built for.         */
+const char* hier_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIERATTN_H */

@@ -1,0 +1,118 @@
+"""ctypes binding of the C ABI in ``include/hierattn.h``.
+
+The library is loaded from ``multics_amd/_lib/libhierattn.so`` (built in tree
+by ``multics_amd.build``).  There is no fallback: when the library is missing
+the import of a compute entry point raises.  Error codes map back to the
+exception types the reference raises for the same conditions
+(multics/models/kernels/hier_segmented_attention.py:425-431 NotImplementedError,
+multics/models/attention.py:500-506 ValueError,
+multics/models/kernels/hier_paged_attention.py:37-47 RuntimeError,
+multics/models/kernels/hier_packed_attention.py:54-64 AssertionError).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhierattn.so"
+
+HIER_OK, HIER_EINVAL, HIER_EUNSUPPORTED, HIER_ELAUNCH, HIER_EINTERNAL = 0, -1, -2, -3, -4
+
+i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
+
+
+class HierTopo(C.Structure):
+    _fields_ = [(n, i32) for n in ("P", "N", "L", "KL", "KG", "n_frames", "n_block",
+                                   "local_attn", "direct", "no_local", "use_membership", "B",
+                                   "fa_max", "fl_max", "fg_max", "T_mem")] + \
+               [(n, vp) for n in ("fa", "fl", "fg", "agent_frames", "local_frames",
+                                  "global_frames", "local_active", "q_frames", "labels",
+                                  "q_active", "membership", "global_only", "ref_agent_base",
+                                  "ref_local_base", "ref_global_base", "tile_agent_base",
+                                  "tile_local_base", "tile_global_base", "ref_qbase",
+                                  "tile_qbase")] + \
+               [("ref_qstride", i32 * 3), ("tile_qstride", i32 * 3)]
+
+
+class HierMetaCounts(C.Structure):
+    _fields_ = [(n, vp) for n in ("seg_count", "tiled_count", "dense_count", "logical_count",
+                                  "tile_count")]
+
+
+class HierMetaOut(C.Structure):
+    _fields_ = [("block_m", i32)] + \
+               [(n, vp) for n in ("seg_prog_off", "seg_kv_off", "seg_max_k", "seg_prog_qbase",
+                                  "seg_prog_nq", "seg_prog_seg", "seg_kv_index", "seg_kv_count",
+                                  "tiled_prog_off", "tiled_kv_off", "tiled_max_k",
+                                  "tiled_prog_qbase", "tiled_prog_nq", "tiled_prog_seg",
+                                  "tiled_kv_index", "tiled_kv_valid", "tiled_kv_count",
+                                  "tile_kv_off", "tile_item_off")] + \
+               [("rows_per_item", i32)] + \
+               [(n, vp) for n in ("tile_kv_idx", "tile_kv_mask", "tile_blk_and", "tile_items")]
+
+
+class HierPrologueArgs(C.Structure):
+    _fields_ = [("S", i32), ("H", i32), ("D", i32), ("eps", f32)] + \
+               [(n, vp) for n in ("qx", "kx", "vx", "cam", "w_cam_q", "w_cam_k")] + \
+               [("C", i32)] + \
+               [(n, vp) for n in ("norm_q_w", "norm_k_w", "rope_cos", "rope_sin", "q_out",
+                                  "k_out", "v_out")] + \
+               [("out_stride_s", i64), ("out_stride_h", i64)]
+
+
+class HierFwdArgs(C.Structure):
+    _fields_ = [("H", i32), ("D", i32), ("n_items", i32), ("scale", f32)] + \
+               [(n, vp) for n in ("q", "k", "v", "o", "lse")] + \
+               [(n, i64) for n in ("q_ss", "q_sh", "k_ss", "k_sh", "v_ss", "v_sh", "o_ss", "o_sh",
+                                   "lse_stride_h")] + \
+               [(n, vp) for n in ("tile_items", "tile_kv_idx", "tile_kv_mask", "tile_blk_and")]
+
+
+EXPORTS = {
+    "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
+    "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
+    "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
+    "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
+    "hier_last_error": [],
+    "hier_version": [],
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"hierattn HIP library not built: {LIB_PATH} is missing "
+                    "(run `python -m multics_amd.build` or __graft_entry__.build())")
+            handle = C.CDLL(str(LIB_PATH))
+            for name, argtypes in EXPORTS.items():
+                fn = getattr(handle, name)
+                fn.argtypes = argtypes
+                fn.restype = C.c_char_p if name in ("hier_last_error", "hier_version") else C.c_int
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == HIER_OK:
+        return
+    msg = f"{what}: {lib().hier_last_error().decode(errors='replace')}"
+    if rc == HIER_EINVAL:
+        raise ValueError(msg)
+    if rc == HIER_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    if rc == HIER_EINTERNAL:
+        raise AssertionError(msg)
+    raise RuntimeError(msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)

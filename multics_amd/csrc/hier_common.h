@@ -1,0 +1,39 @@
+// Shared helpers for the hierattn HIP library: error reporting and launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "hierattn.h"
+
+namespace hier {
+
+// Thread-local last error message, read through hier_last_error().
+extern thread_local char g_last_error[512];
+
+inline int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+inline void clear_error() { g_last_error[0] = 0; }
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(HIER_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return HIER_OK;
+}
+
+}  // namespace hier
+
+#define HIER_REQUIRE(cond, code, ...) \
+  do {                                \
+    if (!(cond)) return ::hier::fail(code, __VA_ARGS__); \
+  } while (0)

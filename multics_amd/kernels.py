@@ -1,0 +1,172 @@
+"""Launchers of the HIP attention kernels under the reference's plugin names.
+
+``hierarchical_tiled_full_sequence_attention`` keeps the reference signature
+(multics/models/kernels/hier_tiled_attention.py:734-796) and error behaviour;
+the layouts it receives come from this package's
+``build_hier_tiled_full_sequence_layouts`` and carry the tile list of the HIP
+forward, so all temporal blocks run in one launch.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from . import _capi
+from .metadata import HierTiledBlockLayout, TileList
+
+
+def _stream(dev) -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _rows_view(t: torch.Tensor):
+    """(tensor, token stride, head stride) of a [S,H,D] / [1,S,H,D] bf16 tensor."""
+    if t.dim() == 4:
+        if t.shape[0] != 1:
+            raise NotImplementedError("hierarchical attention supports B=1")
+        t = t[0]
+    if t.dim() != 3:
+        raise ValueError(f"expected [S,H,D] or [1,S,H,D], got {tuple(t.shape)}")
+    if t.stride(2) != 1:
+        t = t.contiguous()
+    return t, t.stride(0), t.stride(1)
+
+
+def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tiles: TileList,
+                           out: torch.Tensor, *, lse: Optional[torch.Tensor] = None,
+                           item_range: Optional[tuple] = None,
+                           scale: Optional[float] = None) -> torch.Tensor:
+    """Run ``hier_attn_fwd`` over (a range of) the work items of ``tiles``.
+
+    ``q`` / ``out`` rows are addressed by the tile list's query rows, ``k`` / ``v``
+    rows by its key indices; all are bf16 with a unit-stride head dimension.
+    ``lse`` (optional, fp32 [H, S_q]) receives the natural-log softmax normaliser.
+    """
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+        if t.dtype != torch.bfloat16:
+            raise NotImplementedError(f"{name} must be bf16, got {t.dtype}")
+        if not t.is_cuda:
+            raise NotImplementedError("hierarchical attention requires a GPU tensor")
+    q3, q_ss, q_sh = _rows_view(q)
+    k3, k_ss, k_sh = _rows_view(k)
+    v3, v_ss, v_sh = _rows_view(v)
+    o3, o_ss, o_sh = _rows_view(out)
+    if o3.data_ptr() != (out[0] if out.dim() == 4 else out).data_ptr():
+        raise ValueError("out must have a unit-stride head dimension")
+    H, D = q3.shape[1], q3.shape[2]
+    if k3.shape[1:] != (H, D) or v3.shape[1:] != (H, D) or o3.shape[1:] != (H, D):
+        raise ValueError("q/k/v/out head shapes differ")
+    if tiles.rows_per_item != 128:
+        raise ValueError("hier_attn_fwd processes work items of exactly 128 query rows")
+    if k3.shape[0] < tiles.key_extent or v3.shape[0] < tiles.key_extent:
+        raise ValueError(f"K/V hold {k3.shape[0]} rows, the tile list addresses {tiles.key_extent}")
+    if q3.shape[0] < tiles.row_extent or o3.shape[0] < tiles.row_extent:
+        raise ValueError(f"Q/out hold {q3.shape[0]} rows, the tile list addresses {tiles.row_extent}")
+    if lse is not None and (lse.dtype != torch.float32 or lse.dim() != 2 or lse.shape[0] != H
+                            or lse.shape[1] < tiles.row_extent or lse.stride(1) != 1):
+        raise ValueError("lse must be fp32 [H, >=rows] with unit row stride")
+    first, last = item_range if item_range is not None else (0, tiles.n_items)
+    if last <= first:
+        return out
+    args = _capi.HierFwdArgs(
+        H=H, D=D, n_items=last - first, scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
+        q=q3.data_ptr(), k=k3.data_ptr(), v=v3.data_ptr(), o=o3.data_ptr(),
+        lse=None if lse is None else lse.data_ptr(),
+        q_ss=q_ss, q_sh=q_sh, k_ss=k_ss, k_sh=k_sh, v_ss=v_ss, v_sh=v_sh, o_ss=o_ss, o_sh=o_sh,
+        lse_stride_h=0 if lse is None else lse.stride(0),
+        tile_items=tiles.items.data_ptr() + first * 8 * 4, tile_kv_idx=tiles.kv_idx.data_ptr(),
+        tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr())
+    _capi.call("hier_attn_fwd", C.byref(args), _stream(q.device))
+    return out
+
+
+def hierarchical_tiled_full_sequence_attention(*, roped_q: torch.Tensor, roped_k: torch.Tensor,
+                                               value: torch.Tensor,
+                                               layouts: Sequence[HierTiledBlockLayout]) -> torch.Tensor:
+    """Blockwise forward on projected full-sequence Q/K/V (reference signature,
+    hier_tiled_attention.py:734-796); returns ``[B, S, H*D]``."""
+    if roped_k.shape != value.shape or roped_q.ndim != 4 or roped_k.ndim != 4:
+        raise ValueError(
+            f"Tiled128 expects Q [B,Sq,H,D] and matching K/V [B,Sk,H,D], "
+            f"got {roped_q.shape}, {roped_k.shape}, {value.shape}")
+    batch, seq_len, heads, head_dim = roped_q.shape
+    if roped_k.shape[0] != batch or roped_k.shape[2:] != (heads, head_dim):
+        raise ValueError(
+            f"Tiled128 Q/K batch/head shapes must match, got {roped_q.shape}, {roped_k.shape}")
+    if batch != 1 or head_dim not in (64, 128) or roped_q.dtype != torch.bfloat16:
+        raise NotImplementedError(
+            "hierarchical attention supports B=1, BF16, head_dim 64/128; "
+            f"got B={batch}, dtype={roped_q.dtype}, head_dim={head_dim}")
+    if not roped_q.is_cuda:
+        raise NotImplementedError("hierarchical attention requires a GPU tensor")
+    if roped_k.dtype != roped_q.dtype or value.dtype != roped_q.dtype:
+        raise ValueError("Tiled128 Q/K/V dtypes must match")
+    out = torch.zeros_like(roped_q)
+    if not layouts:
+        return out.reshape(batch, seq_len, heads * head_dim)
+    tiles = layouts[0].tiles
+    if tiles is None or any(l.tiles is not tiles for l in layouts):
+        raise ValueError("layouts must come from one build_hier_tiled_full_sequence_layouts call")
+    blocks = sorted(l.block for l in layouts)
+    if blocks == list(range(len(tiles.item_ranges))):
+        hier_attention_forward(roped_q, roped_k, value, tiles, out)
+    else:
+        for b in blocks:
+            hier_attention_forward(roped_q, roped_k, value, tiles, out,
+                                   item_range=tiles.item_ranges[b])
+    return out.reshape(batch, seq_len, heads * head_dim)
+
+
+def qkv_prologue(qx: torch.Tensor, kx: torch.Tensor, vx: Optional[torch.Tensor], *,
+                 norm_q_w: torch.Tensor, norm_k_w: torch.Tensor, rope_cos: torch.Tensor,
+                 rope_sin: torch.Tensor, num_heads: int, eps: float,
+                 cam: Optional[torch.Tensor] = None, w_cam_q: Optional[torch.Tensor] = None,
+                 w_cam_k: Optional[torch.Tensor] = None, out_layout: str = "shd"):
+    """Fused camera adapter + RMSNorm + gain + RoPE (``hier_qkv_prologue``).
+
+    Inputs are ``[S, H*D]`` bf16 projections; returns ``(q, k, v)`` bf16 as
+    ``[S, H, D]`` (``out_layout="shd"``) or head-major ``[H, S, D]`` views
+    presented as ``[S, H, D]`` (``"hsd"``).  ``v`` is None when ``vx`` is None.
+    """
+    S, dim = qx.shape
+    H = int(num_heads)
+    D = dim // H
+    dev = qx.device
+    for t in (qx, kx) + ((vx,) if vx is not None else ()):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.shape != (S, dim):
+            raise ValueError("projections must be contiguous bf16 [S, H*D]")
+    if out_layout == "shd":
+        mk = lambda: torch.empty((S, H, D), dtype=torch.bfloat16, device=dev)
+        q, k = mk(), mk()
+        v = mk() if vx is not None else None
+        ss, sh = H * D, D
+    elif out_layout == "hsd":
+        mk = lambda: torch.empty((H, S, D), dtype=torch.bfloat16, device=dev)
+        qh, kh = mk(), mk()
+        vh = mk() if vx is not None else None
+        q, k = qh.permute(1, 0, 2), kh.permute(1, 0, 2)
+        v = vh.permute(1, 0, 2) if vh is not None else None
+        ss, sh = D, S * D
+    else:
+        raise ValueError(f"unknown layout {out_layout!r}")
+    nw = [x.contiguous() for x in (norm_q_w, norm_k_w)]
+    cs = rope_cos.contiguous().float()
+    sn = rope_sin.contiguous().float()
+    if cs.shape != (S, D // 2) or sn.shape != (S, D // 2):
+        raise ValueError(f"rope tables must be [S, D/2] = {(S, D // 2)}, got {tuple(cs.shape)}")
+    camc = None if cam is None else cam.to(torch.bfloat16).contiguous()
+    wq = None if w_cam_q is None else w_cam_q.to(torch.bfloat16).contiguous()
+    wk = None if w_cam_k is None else w_cam_k.to(torch.bfloat16).contiguous()
+    args = _capi.HierPrologueArgs(
+        S=S, H=H, D=D, eps=float(eps), qx=qx.data_ptr(), kx=kx.data_ptr(),
+        vx=None if vx is None else vx.data_ptr(), cam=None if camc is None else camc.data_ptr(),
+        w_cam_q=None if wq is None else wq.data_ptr(), w_cam_k=None if wk is None else wk.data_ptr(),
+        C=0 if camc is None else camc.shape[-1], norm_q_w=nw[0].data_ptr(), norm_k_w=nw[1].data_ptr(),
+        rope_cos=cs.data_ptr(), rope_sin=sn.data_ptr(), q_out=q.data_ptr(), k_out=k.data_ptr(),
+        v_out=None if v is None else v.data_ptr(), out_stride_s=ss, out_stride_h=sh)
+    _capi.call("hier_qkv_prologue", C.byref(args), _stream(dev))
+    return q, k, v

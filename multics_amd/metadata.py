@@ -1,0 +1,633 @@
+"""Device metadata builder: hierarchical topology -> key lists and tile lists.
+
+Host side of ``hier_meta_count`` / ``hier_meta_build`` (``include/hierattn.h``).
+The host only lays out tiny per-stream address tables (the token offset of every
+cached frame); the edge rule itself -- which frames of which stream each query
+segment may read -- is evaluated on the GPU, which then expands and packs:
+
+* ``SegmentedMetadata`` -- the tuple returned by the reference's
+  ``_build_metadata`` (multics/models/kernels/hier_segmented_attention.py:156-395),
+  bit-exact;
+* ``HierTiledBlockLayout`` -- the reference's Tiled128 layout dataclass
+  (hier_tiled_attention.py:37-49, 182-655), bit-exact, with a handle to
+* ``TileList`` -- this library's attention work list: per (block, stream) the
+  ordered union of the per-frame key lists with a visibility bitmask per key.
+
+Two-pass sizing: the count pass is followed by one small device-to-host copy
+(the counts), exactly where the reference's own builder runs on the host, and
+results are cached in bounded LRU caches keyed by the topology values, like the
+reference's (hier_segmented_attention.py:22-24, 137-153;
+hier_tiled_attention.py:165-179).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+from collections import OrderedDict
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _capi
+
+TILE_KEYS = 64          # attention kernel key tile
+ROWS_PER_ITEM = 128     # attention kernel query rows per work item
+SEG_ROUND = 64          # hier_segmented_attention.py:371
+TILED_N = 128           # hier_tiled_attention.py:33
+TILED_M = 16            # hier_tiled_attention.py:32
+
+
+def _ceil(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+@dataclass
+class TileList:
+    """Work list consumed by ``hier_attn_fwd`` (device tensors)."""
+
+    items: torch.Tensor          # [n_items, 8] int32
+    kv_idx: torch.Tensor         # [n_keys] int32
+    kv_mask: torch.Tensor        # [n_keys] int32 (uint32 bits)
+    blk_and: torch.Tensor        # [n_keys / 64] int32 (uint32 bits)
+    n_items: int
+    item_ranges: tuple           # per block: (first item, end item)
+    logical_pairs: int           # useful (q, k) pairs (FLOP accounting)
+    key_extent: int = 0          # 1 + largest K/V row index any key can address
+    row_extent: int = 0          # 1 + largest Q/O row index any item can address
+    rows_per_item: int = ROWS_PER_ITEM
+
+
+@dataclass(frozen=True)
+class HierTiledBlockLayout:
+    """Same fields as the reference dataclass (hier_tiled_attention.py:37-49)."""
+
+    prog_qbase: torch.Tensor
+    prog_nq: torch.Tensor
+    prog_seg: torch.Tensor
+    kv_index: torch.Tensor
+    kv_valid: torch.Tensor
+    kv_count: torch.Tensor
+    logical_slots: int
+    physical_slots: int
+    dense_slots: int
+    tiles: Optional[TileList] = field(default=None, compare=False, repr=False)
+    block: int = field(default=0, compare=False, repr=False)
+
+
+@dataclass
+class BuildResult:
+    tiles: TileList
+    segmented: Optional[list]     # per block: (qbase, nq, seg, kv_index, kv_count, pairs)
+    tiled: Optional[list]         # per block: HierTiledBlockLayout
+    seg_counts: torch.Tensor      # [B, n_seg] (cpu)
+
+
+# --------------------------------------------------------------------------
+# topology description
+# --------------------------------------------------------------------------
+
+@dataclass
+class BlockTopology:
+    """Inputs of the builder for B blocks, as host numpy arrays.
+
+    Frame lists are per block and per stream kind (equal lengths inside a
+    block, as the reference requires: hier_segmented_attention.py:185-202).
+    """
+
+    P: int
+    N: int
+    L: int
+    KL: int
+    KG: int
+    n_frames: int
+    n_block: int
+    local_attn: int
+    direct: bool
+    no_local: bool
+    agent_frames: list            # B x [P][fa]
+    local_frames: list            # B x [N][fl]
+    global_frames: list           # B x [fg]
+    local_active: list            # B x [N][fl] bool
+    q_frames: list                # B x [n]
+    q_active: list                # B x [n][N] bool
+    labels: Optional[list] = None         # B x [n][P]
+    membership: Optional[np.ndarray] = None   # [T][N][P] bool
+    global_only: Optional[np.ndarray] = None  # [T][P] bool
+    # addressing
+    ref_agent_base: list = None   # B x [P][fa]
+    ref_local_base: list = None
+    ref_global_base: list = None
+    tile_agent_base: list = None
+    tile_local_base: list = None
+    tile_global_base: list = None
+    ref_qbase: list = None        # B x [P+N+1]
+    tile_qbase: list = None
+    ref_qstride: tuple = (0, 0, 0)
+    tile_qstride: tuple = (0, 0, 0)
+
+    @property
+    def B(self) -> int:
+        return len(self.agent_frames)
+
+    @property
+    def n_seg(self) -> int:
+        return self.n_frames * (self.P + (0 if self.no_local else self.N) + 1)
+
+    def validate(self) -> None:
+        P, N, n = self.P, self.N, self.n_frames
+        if not 1 <= n <= 32:
+            raise NotImplementedError(f"n_frames must be in [1, 32], got {n}")
+        if self.no_local and self.KL != 0:
+            raise ValueError("hier_no_local_hub metadata requires K_L=0 and empty local caches")
+        T_mem = None if self.membership is None else self.membership.shape[0]
+        for b in range(self.B):
+            af = self.agent_frames[b]
+            if len(af) != P or any(len(x) != len(af[0]) for x in af):
+                raise ValueError("segmented hierarchical attention requires equal agent cache lengths")
+            if not self.no_local:
+                lf = self.local_frames[b]
+                if len(lf) != N or any(len(x) != len(lf[0]) for x in lf):
+                    raise ValueError("segmented hierarchical attention requires equal local cache lengths")
+            for row in list(af) + list(self.local_frames[b]) + [self.global_frames[b]]:
+                r = np.asarray(row, dtype=np.int64)
+                if r.size and (r.min() < 0 or np.any(np.diff(r) <= 0)):
+                    raise ValueError("cached frame ids must be non-negative and strictly increasing")
+            for p in range(P):
+                if self.direct and any(f not in set(af[p]) for f in self.q_frames[b]):
+                    raise ValueError("every agent cache must hold the current query frames")
+            if T_mem is not None:
+                allf = [f for row in af for f in row] + list(self.q_frames[b])
+                if max(allf, default=0) >= T_mem:
+                    raise ValueError(f"membership T={T_mem} does not cover the cached frames")
+
+
+def _cached_pool_bases(P, N, L, KL, KG, fa, fl, fg):
+    """Token offsets of the reference's concatenated cache pool (hier_segmented_attention.py:247-258)."""
+    agent = [[(p * fa + fi) * L for fi in range(fa)] for p in range(P)]
+    local_start = P * fa * L
+    local = [[local_start + (g * fl + fi) * KL for fi in range(fl)] for g in range(N)]
+    glob0 = local_start + N * fl * KL
+    glob = [glob0 + fi * KG for fi in range(fg)]
+    return agent, local, glob
+
+
+def cached_topology(*, P, N, L, KL, KG, n_frames, n_block, local_attn, agent_frame_lists,
+                    local_frame_lists, global_frame_list, local_active_frames, labels, q_active,
+                    direct_player, membership=None, global_only=None, hier_no_local_hub=False,
+                    tile_bases=None, tile_qbase=None, tile_qstride=None) -> BlockTopology:
+    """One cached call (B = 1) in the reference's cached pool and query order."""
+    no_local = bool(hier_no_local_hub)
+    fa = len(agent_frame_lists[0])
+    fl = 0 if no_local else len(local_frame_lists[0])
+    fg = len(global_frame_list)
+    n = int(n_frames)
+    qf = tuple(global_frame_list[-n:]) if KG > 0 else ()
+    if len(qf) != n:
+        qf = tuple(agent_frame_lists[0][-n:])
+    if len(qf) != n:
+        raise ValueError("segmented hierarchical attention cannot identify the current query frames")
+    agent, local, glob = _cached_pool_bases(P, N, L, KL, KG, fa, fl, fg)
+    aq = P * n * L
+    ref_qbase = [p * n * L for p in range(P)] + [aq + g * KL for g in range(N)] + [aq + n * N * KL]
+    ref_qstride = (L, N * KL, KG)
+    if membership is not None:
+        membership = np.asarray(membership, dtype=bool)
+        if global_only is None:
+            raise ValueError("membership metadata requires global_only")
+        global_only = np.asarray(global_only, dtype=bool)
+    tb = tile_bases or (agent, local, glob)
+    return BlockTopology(
+        P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=int(n_block),
+        local_attn=int(local_attn), direct=bool(direct_player), no_local=no_local,
+        agent_frames=[[list(x) for x in agent_frame_lists]],
+        local_frames=[[list(x) for x in local_frame_lists] if not no_local else []],
+        global_frames=[list(global_frame_list)],
+        local_active=[[list(map(bool, x)) for x in local_active_frames] if not no_local else []],
+        q_frames=[list(qf)],
+        q_active=[[list(map(bool, r)) for r in q_active]],
+        labels=None if labels is None else [[list(map(int, r)) for r in labels]],
+        membership=membership, global_only=global_only,
+        ref_agent_base=[agent], ref_local_base=[local], ref_global_base=[glob],
+        tile_agent_base=[tb[0]], tile_local_base=[tb[1]], tile_global_base=[tb[2]],
+        ref_qbase=[ref_qbase], tile_qbase=[tile_qbase or ref_qbase],
+        ref_qstride=ref_qstride, tile_qstride=tile_qstride or ref_qstride,
+    )
+
+
+def full_sequence_topology(*, P, T, L, N, KL, KG, n, window, direct, labels=None, active=None,
+                           membership=None, global_only=None, no_local=False) -> BlockTopology:
+    """All T/n temporal blocks of a full training/inference sequence.
+
+    Block b queries frames [b*n, b*n+n) and reads the frames a rolling cache of
+    W+n frames would hold (hier_tiled_attention.py:307-333), addressed in the
+    full-sequence token order [P*T*L | T*N*KL | T*KG] (hier_masks.py:549-571).
+    """
+    if T % n != 0:
+        raise ValueError(f"Tiled128 requires T % n == 0, got T={T}, n={n}")
+    if window != -1 and window < n:
+        raise ValueError(f"Tiled128 requires local_attn_size=-1 or >=n, got {window}, n={n}")
+    if membership is not None:
+        mem = np.asarray(membership, dtype=bool).reshape(T, N, P)
+        if global_only is None:
+            raise ValueError("membership metadata requires global_only")
+        go = np.asarray(global_only, dtype=bool).reshape(T, P)
+        act = mem.any(-1) if active is None else np.asarray(active, dtype=bool).reshape(T, N)
+        lab = None
+    else:
+        lab = np.asarray(labels, dtype=np.int64).reshape(T, P)
+        if lab.size and (lab.min() < 0 or lab.max() >= N):
+            raise ValueError(f"group_labels values must be in [0,{N})")
+        if active is None:
+            act = np.zeros((T, N), dtype=bool)
+            act[np.arange(T)[:, None], lab] = True
+        else:
+            act = np.asarray(active, dtype=bool).reshape(T, N)
+        mem = go = None
+    retention = T if window == -1 else window + n
+    local_start = P * T * L
+    global_start = local_start + T * N * KL
+    A, Lo, G, AF, LF, GF, LA, QF, QA, LB, RQ = ([] for _ in range(11))
+    for b in range(T // n):
+        b0, b1 = b * n, b * n + n
+        kept = list(range(max(0, b1 - retention), b1))
+        AF.append([kept] * P)
+        LF.append([] if no_local else [kept] * N)
+        GF.append(kept)
+        LA.append([] if no_local else [[bool(act[f, g]) for f in kept] for g in range(N)])
+        QF.append(list(range(b0, b1)))
+        QA.append([[bool(act[f, g]) for g in range(N)] for f in range(b0, b1)])
+        if lab is not None:
+            LB.append([[int(x) for x in lab[f]] for f in range(b0, b1)])
+        A.append([[(p * T + f) * L for f in kept] for p in range(P)])
+        Lo.append([] if no_local else [[local_start + (f * N + g) * KL for f in kept] for g in range(N)])
+        G.append([global_start + f * KG for f in kept])
+        RQ.append([(p * T + b0) * L for p in range(P)]
+                  + [local_start + (b0 * N + g) * KL for g in range(N)]
+                  + [global_start + b0 * KG])
+    stride = (L, N * KL, KG)
+    return BlockTopology(
+        P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=n, local_attn=window,
+        direct=bool(direct), no_local=bool(no_local), agent_frames=AF, local_frames=LF,
+        global_frames=GF, local_active=LA, q_frames=QF, q_active=QA,
+        labels=LB if lab is not None else None, membership=mem, global_only=go,
+        ref_agent_base=A, ref_local_base=Lo, ref_global_base=G,
+        tile_agent_base=A, tile_local_base=Lo, tile_global_base=G,
+        ref_qbase=RQ, tile_qbase=RQ, ref_qstride=stride, tile_qstride=stride)
+
+
+# --------------------------------------------------------------------------
+# device build
+# --------------------------------------------------------------------------
+
+def _pad3(rows_per_block, inner, width, dtype=np.int32):
+    """B x [inner][<=width] ragged lists -> dense [B, inner, width] array."""
+    B = len(rows_per_block)
+    out = np.zeros((B, max(inner, 1), max(width, 1)), dtype=dtype)
+    for b, rows in enumerate(rows_per_block):
+        for i, r in enumerate(rows):
+            out[b, i, :len(r)] = r
+    return out
+
+
+def _pad2(rows, width, dtype=np.int32):
+    out = np.zeros((len(rows), max(width, 1)), dtype=dtype)
+    for b, r in enumerate(rows):
+        out[b, :len(r)] = r
+    return out
+
+
+def _qlen(topo: BlockTopology, s: int) -> int:
+    if s < topo.P:
+        return topo.L
+    if s < topo.P + topo.N:
+        return 0 if topo.no_local else topo.KL
+    return topo.KG
+
+
+def _seg_qlens(topo: BlockTopology) -> np.ndarray:
+    n = topo.n_frames
+    q = [topo.L] * (topo.P * n)
+    if not topo.no_local:
+        q += [topo.KL] * (n * topo.N)
+    q += [topo.KG] * n
+    return np.asarray(q, dtype=np.int64)
+
+
+def _progs_per_block(topo: BlockTopology, bm: int) -> int:
+    return int(sum(_ceil(int(x), bm) for x in _seg_qlens(topo)))
+
+
+def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
+          tiled: bool = False, rows_per_item: int = ROWS_PER_ITEM) -> BuildResult:
+    """Run the two device passes and return device tensors."""
+    topo.validate()
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise NotImplementedError("the hierarchical metadata builder runs on the GPU (HIP)")
+    P, N, n, B = topo.P, topo.N, topo.n_frames, topo.B
+    NS = P + N + 1
+    fa = [len(x[0]) for x in topo.agent_frames]
+    fl = [0 if topo.no_local else len(x[0]) for x in topo.local_frames]
+    fg = [len(x) for x in topo.global_frames]
+    fa_max, fl_max, fg_max = max(fa), max(fl + [0]), max(fg + [0])
+    use_mem = topo.membership is not None
+    T_mem = topo.membership.shape[0] if use_mem else 0
+
+    host = {
+        "fa": np.asarray(fa, np.int32), "fl": np.asarray(fl, np.int32), "fg": np.asarray(fg, np.int32),
+        "agent_frames": _pad3(topo.agent_frames, P, fa_max),
+        "local_frames": _pad3(topo.local_frames, N, fl_max),
+        "global_frames": _pad2(topo.global_frames, fg_max),
+        "local_active": _pad3(topo.local_active, N, fl_max, np.uint8),
+        "q_frames": np.asarray(topo.q_frames, np.int32).reshape(B, n),
+        "q_active": np.asarray(topo.q_active, np.uint8).reshape(B, n, N),
+        "labels": (np.asarray(topo.labels, np.int32).reshape(B, n, P) if topo.labels is not None
+                   else np.zeros((1,), np.int32)),
+        "membership": (np.ascontiguousarray(topo.membership, dtype=np.uint8) if use_mem
+                       else np.zeros((1,), np.uint8)),
+        "global_only": (np.ascontiguousarray(topo.global_only, dtype=np.uint8) if use_mem
+                        else np.zeros((1,), np.uint8)),
+        "ref_agent_base": _pad3(topo.ref_agent_base, P, fa_max),
+        "ref_local_base": _pad3(topo.ref_local_base, N, fl_max),
+        "ref_global_base": _pad2(topo.ref_global_base, fg_max),
+        "tile_agent_base": _pad3(topo.tile_agent_base, P, fa_max),
+        "tile_local_base": _pad3(topo.tile_local_base, N, fl_max),
+        "tile_global_base": _pad2(topo.tile_global_base, fg_max),
+        "ref_qbase": np.asarray(topo.ref_qbase, np.int32).reshape(B, NS),
+        "tile_qbase": np.asarray(topo.tile_qbase, np.int32).reshape(B, NS),
+    }
+    dv = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in host.items()}
+    t = _capi.HierTopo(P=P, N=N, L=topo.L, KL=topo.KL, KG=topo.KG, n_frames=n,
+                       n_block=topo.n_block, local_attn=topo.local_attn, direct=int(topo.direct),
+                       no_local=int(topo.no_local), use_membership=int(use_mem), B=B,
+                       fa_max=fa_max, fl_max=fl_max, fg_max=fg_max, T_mem=T_mem)
+    for k, v in dv.items():
+        setattr(t, k, v.data_ptr())
+    if topo.labels is None:
+        t.labels = None
+    if not use_mem:
+        t.membership = t.global_only = None
+    t.ref_qstride = (C.c_int32 * 3)(*topo.ref_qstride)
+    t.tile_qstride = (C.c_int32 * 3)(*topo.tile_qstride)
+    stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    n_seg = topo.n_seg
+    seg_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
+    til_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
+    den_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
+    log_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
+    tile_c = torch.zeros((B, NS), dtype=torch.int32, device=dev)
+    counts = _capi.HierMetaCounts(seg_count=seg_c.data_ptr(), tiled_count=til_c.data_ptr(),
+                                  dense_count=den_c.data_ptr(), logical_count=log_c.data_ptr(),
+                                  tile_count=tile_c.data_ptr())
+    _capi.call("hier_meta_count", C.byref(t), C.byref(counts), stream)
+    seg_h, til_h, den_h, log_h, tile_h = (x.cpu().numpy().astype(np.int64)
+                                          for x in (seg_c, til_c, den_c, log_c, tile_c))
+
+    out = _capi.HierMetaOut()
+    keep = []
+
+    def dbuf(arr, dtype=torch.int64):
+        x = torch.as_tensor(np.asarray(arr), dtype=dtype).to(dev)
+        keep.append(x)
+        return x
+
+    # ---- tile list ----------------------------------------------------------
+    tile_off = np.concatenate([[0], np.cumsum(tile_h.reshape(-1))])
+    n_keys = int(tile_off[-1])
+    rows = np.array([[n * _qlen(topo, s) for s in range(NS)] for _ in range(B)], dtype=np.int64)
+    nit = -(-rows // rows_per_item)
+    item_off = np.concatenate([[0], np.cumsum(nit.reshape(-1))])
+    n_items = int(item_off[-1])
+    kv_idx = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
+    kv_mask = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
+    blk_and = torch.empty(max(n_keys // TILE_KEYS, 1), dtype=torch.int32, device=dev)
+    items = torch.empty((max(n_items, 1), 8), dtype=torch.int32, device=dev)
+    out.tile_kv_off = dbuf(tile_off[:-1]).data_ptr()
+    out.tile_item_off = dbuf(item_off[:-1], torch.int32).data_ptr()
+    out.rows_per_item = rows_per_item
+    out.tile_kv_idx, out.tile_kv_mask = kv_idx.data_ptr(), kv_mask.data_ptr()
+    out.tile_blk_and, out.tile_items = blk_and.data_ptr(), items.data_ptr()
+
+    qlens = _seg_qlens(topo)
+    pairs = (seg_h * qlens[None, :]).sum(1)
+
+    # ---- _build_metadata arrays ---------------------------------------------
+    seg_res = None
+    if segmented_block_m is not None:
+        bm = int(segmented_block_m)
+        maxk = np.array([_ceil(max(int(seg_h[b].max(initial=0)), 1), SEG_ROUND) * SEG_ROUND
+                         for b in range(B)])
+        kv_off = np.concatenate([[0], np.cumsum(maxk * n_seg)])
+        npb = _progs_per_block(topo, bm)
+        prog_off = np.arange(B + 1, dtype=np.int64) * npb
+        s_kv = torch.empty(max(int(kv_off[-1]), 1), dtype=torch.int32, device=dev)
+        s_cnt = torch.empty(B * n_seg, dtype=torch.int32, device=dev)
+        s_pq = torch.empty(max(B * npb, 1), dtype=torch.int32, device=dev)
+        s_pn = torch.empty_like(s_pq)
+        s_ps = torch.empty_like(s_pq)
+        out.block_m = bm
+        out.seg_prog_off = dbuf(prog_off[:-1]).data_ptr()
+        out.seg_kv_off = dbuf(kv_off[:-1]).data_ptr()
+        out.seg_max_k = dbuf(maxk, torch.int32).data_ptr()
+        out.seg_prog_qbase, out.seg_prog_nq, out.seg_prog_seg = (s_pq.data_ptr(), s_pn.data_ptr(),
+                                                                 s_ps.data_ptr())
+        out.seg_kv_index, out.seg_kv_count = s_kv.data_ptr(), s_cnt.data_ptr()
+        seg_res = [(s_pq[b * npb:(b + 1) * npb], s_pn[b * npb:(b + 1) * npb],
+                    s_ps[b * npb:(b + 1) * npb],
+                    s_kv[int(kv_off[b]):int(kv_off[b + 1])].view(n_seg, int(maxk[b])),
+                    s_cnt[b * n_seg:(b + 1) * n_seg], int(pairs[b])) for b in range(B)]
+
+    # ---- Tiled128 arrays ----------------------------------------------------
+    tiled_res = None
+    if tiled:
+        if topo.membership is not None or topo.no_local:
+            raise ValueError("Tiled128 layouts are defined for the labels topology with local hubs")
+        maxk = np.array([_ceil(max(int(til_h[b].max(initial=0)), 1), TILED_N) * TILED_N
+                         for b in range(B)])
+        kv_off = np.concatenate([[0], np.cumsum(maxk * n_seg)])
+        npb = _progs_per_block(topo, TILED_M)
+        prog_off = np.arange(B + 1, dtype=np.int64) * npb
+        t_kv = torch.empty(max(int(kv_off[-1]), 1), dtype=torch.int32, device=dev)
+        t_va = torch.empty(max(int(kv_off[-1]), 1), dtype=torch.uint8, device=dev)
+        t_cnt = torch.empty(B * n_seg, dtype=torch.int32, device=dev)
+        t_pq = torch.empty(max(B * npb, 1), dtype=torch.int32, device=dev)
+        t_pn = torch.empty_like(t_pq)
+        t_ps = torch.empty_like(t_pq)
+        out.tiled_prog_off = dbuf(prog_off[:-1]).data_ptr()
+        out.tiled_kv_off = dbuf(kv_off[:-1]).data_ptr()
+        out.tiled_max_k = dbuf(maxk, torch.int32).data_ptr()
+        out.tiled_prog_qbase, out.tiled_prog_nq, out.tiled_prog_seg = (
+            t_pq.data_ptr(), t_pn.data_ptr(), t_ps.data_ptr())
+        out.tiled_kv_index, out.tiled_kv_valid = t_kv.data_ptr(), t_va.data_ptr()
+        out.tiled_kv_count = t_cnt.data_ptr()
+        tiled_res = []
+        for b in range(B):
+            tiled_res.append(dict(
+                prog_qbase=t_pq[b * npb:(b + 1) * npb], prog_nq=t_pn[b * npb:(b + 1) * npb],
+                prog_seg=t_ps[b * npb:(b + 1) * npb],
+                kv_index=t_kv[int(kv_off[b]):int(kv_off[b + 1])].view(n_seg, int(maxk[b])),
+                kv_valid=t_va[int(kv_off[b]):int(kv_off[b + 1])].view(n_seg, int(maxk[b])),
+                kv_count=t_cnt[b * n_seg:(b + 1) * n_seg],
+                logical_slots=int(log_h[b].sum()), physical_slots=int(til_h[b].sum()),
+                dense_slots=int(den_h[b].sum())))
+
+    _capi.call("hier_meta_build", C.byref(t), C.byref(out), stream)
+
+    ranges = tuple((int(item_off[b * NS]), int(item_off[(b + 1) * NS])) for b in range(B))
+    key_ext = 0
+    for b in range(B):
+        for rows_, w in ((topo.tile_agent_base[b], topo.L), (topo.tile_local_base[b], topo.KL),
+                         (topo.tile_global_base[b], topo.KG)):
+            flat = [x for r in rows_ for x in (r if isinstance(r, (list, tuple)) else [r])]
+            if flat and w > 0:
+                key_ext = max(key_ext, max(flat) + w)
+    row_ext = 0
+    for b in range(B):
+        for s_ in range(NS):
+            ql = _qlen(topo, s_)
+            if ql > 0:
+                kind = 0 if s_ < P else (1 if s_ < P + N else 2)
+                row_ext = max(row_ext, topo.tile_qbase[b][s_] + (n - 1) * topo.tile_qstride[kind] + ql)
+    tiles = TileList(items=items[:n_items], kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
+                     n_items=n_items, item_ranges=ranges, logical_pairs=int(pairs.sum()),
+                     key_extent=int(key_ext), row_extent=int(row_ext),
+                     rows_per_item=rows_per_item)
+    tiles._keepalive = (dv, keep)  # device inputs must outlive the async build
+    layouts = None
+    if tiled_res is not None:
+        layouts = [HierTiledBlockLayout(tiles=tiles, block=b, **d) for b, d in enumerate(tiled_res)]
+    return BuildResult(tiles=tiles, segmented=seg_res, tiled=layouts,
+                       seg_counts=torch.from_numpy(seg_h.astype(np.int32)))
+
+
+# --------------------------------------------------------------------------
+# reference-named entry points with bounded LRU caches
+# --------------------------------------------------------------------------
+
+_META_CACHE: "OrderedDict[tuple, object]" = OrderedDict()
+_LAYOUT_CACHE: "OrderedDict[tuple, object]" = OrderedDict()
+
+
+def _lru_get(cache, key):
+    v = cache.get(key)
+    if v is not None:
+        cache.move_to_end(key)
+    return v
+
+
+def _lru_put(cache, key, value, env, default):
+    n = max(int(os.environ.get(env, default)), 0)
+    if n == 0:
+        return
+    cache[key] = value
+    cache.move_to_end(key)
+    while len(cache) > n:
+        cache.popitem(last=False)
+
+
+def _freeze(x):
+    if x is None:
+        return None
+    if isinstance(x, np.ndarray):
+        return (x.shape, x.tobytes())
+    if torch.is_tensor(x):
+        a = x.detach().cpu().numpy()
+        return (a.shape, a.tobytes())
+    return tuple(_freeze(v) if isinstance(v, (list, tuple, np.ndarray)) else v for v in x)
+
+
+def _build_metadata(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn, agent_frame_lists,
+                    local_frame_lists, global_frame_list, local_active_frames, labels, q_active,
+                    direct_player, block_m, membership=None, global_only=None,
+                    hier_no_local_hub=False, return_tiles=False):
+    """Same arguments and return tuple as the reference
+    (hier_segmented_attention.py:156-395): ``(prog_qbase, prog_nq, prog_seg,
+    kv_index, kv_count, logical_pairs)``; with ``return_tiles`` a seventh
+    element holds the attention kernel's ``TileList`` for the same call.
+    """
+    key = ("seg", str(device), P, N, L, KL, KG, n_frames, n_block, local_attn,
+           _freeze(agent_frame_lists), _freeze(local_frame_lists), _freeze(global_frame_list),
+           _freeze(local_active_frames), _freeze(labels), _freeze(q_active), bool(direct_player),
+           bool(hier_no_local_hub), block_m, _freeze(membership), _freeze(global_only))
+    hit = _lru_get(_META_CACHE, key)
+    if hit is None:
+        topo = cached_topology(
+            P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n_frames, n_block=n_block, local_attn=local_attn,
+            agent_frame_lists=agent_frame_lists, local_frame_lists=local_frame_lists,
+            global_frame_list=global_frame_list, local_active_frames=local_active_frames,
+            labels=labels, q_active=q_active, direct_player=direct_player, membership=membership,
+            global_only=global_only, hier_no_local_hub=hier_no_local_hub)
+        res = build(topo, device, segmented_block_m=block_m)
+        hit = (*res.segmented[0], res.tiles)
+        _lru_put(_META_CACHE, key, hit, "WAN_HIER_SEGMENTED_META_CACHE_SIZE", "64")
+    return hit if return_tiles else hit[:6]
+
+
+def build_hier_tiled_full_sequence_layouts(*, device, num_players, num_frames, num_patches,
+                                           num_groups, num_local_hub_tokens,
+                                           num_global_hub_tokens, num_frame_per_block,
+                                           local_attn_size, group_labels, active_group,
+                                           direct_player):
+    """Same signature and per-block layouts as the reference
+    (hier_tiled_attention.py:244-429); the layouts also carry the tile list
+    the HIP forward consumes (one launch for all blocks)."""
+    P, T, L = int(num_players), int(num_frames), int(num_patches)
+    N, KL, KG = int(num_groups), int(num_local_hub_tokens), int(num_global_hub_tokens)
+    n, window = int(num_frame_per_block), int(local_attn_size)
+    if T % n != 0:
+        raise ValueError(f"Tiled128 requires T % n == 0, got T={T}, n={n}")
+    if window != -1 and window < n:
+        raise ValueError(f"Tiled128 requires local_attn_size=-1 or >=n, got {window}, n={n}")
+    if tuple(group_labels.shape) != (T, P) or tuple(active_group.shape) != (T, N):
+        raise ValueError(
+            "Tiled128 grouping shape mismatch: "
+            f"labels={tuple(group_labels.shape)} expected {(T, P)}, "
+            f"active={tuple(active_group.shape)} expected {(T, N)}")
+    labels = group_labels.detach().to("cpu", torch.long).numpy()
+    active = active_group.detach().to("cpu", torch.bool).numpy()
+    for s in range(0, T, n):
+        if any(not np.array_equal(labels[t], labels[s]) for t in range(s + 1, min(s + n, T))):
+            raise ValueError("Tiled128 requires group labels constant inside each temporal block")
+    key = ("full", str(torch.device(device)), P, T, L, N, KL, KG, n, window, labels.tobytes(),
+           active.tobytes(), bool(direct_player), TILED_M, TILED_N)
+    hit = _lru_get(_LAYOUT_CACHE, key)
+    if hit is None:
+        topo = full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=window,
+                                      direct=direct_player, labels=labels, active=active)
+        hit = tuple(build(topo, device, tiled=True).tiled)
+        _lru_put(_LAYOUT_CACHE, key, hit, "WAN_HIER_TILED_LAYOUT_CACHE_SIZE", "2")
+    return hit
+
+
+def build_hier_tiled_cached_layout(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn,
+                                   agent_frame_lists, local_frame_lists, global_frame_list,
+                                   local_active_frames, labels, q_active, direct_player):
+    """Reference signature (hier_tiled_attention.py:474-655)."""
+    key = ("cached", str(torch.device(device)), P, N, L, KL, KG, n_frames, n_block, local_attn,
+           _freeze(agent_frame_lists), _freeze(local_frame_lists), _freeze(global_frame_list),
+           _freeze(local_active_frames), _freeze(labels), _freeze(q_active), bool(direct_player),
+           TILED_M, TILED_N)
+    hit = _lru_get(_LAYOUT_CACHE, key)
+    if hit is None:
+        topo = cached_topology(
+            P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n_frames, n_block=n_block, local_attn=local_attn,
+            agent_frame_lists=agent_frame_lists, local_frame_lists=local_frame_lists,
+            global_frame_list=global_frame_list, local_active_frames=local_active_frames,
+            labels=labels, q_active=q_active, direct_player=direct_player)
+        hit = (build(topo, device, tiled=True).tiled[0],)
+        _lru_put(_LAYOUT_CACHE, key, hit, "WAN_HIER_TILED_LAYOUT_CACHE_SIZE", "2")
+    return hit[0]
+
+
+def clear_hier_tiled_layout_cache() -> None:
+    """Testing/debug helper (hier_tiled_attention.py:799-801)."""
+    _LAYOUT_CACHE.clear()
+
+
+def clear_metadata_cache() -> None:
+    _META_CACHE.clear()

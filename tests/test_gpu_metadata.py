@@ -1,0 +1,125 @@
+"""HIP metadata builder: bit-exact against the reference's golden vectors.
+
+Segmented lists (``_build_metadata``), cached and full-sequence Tiled128
+layouts, plus the attention tile list's per-row key sets against the golden
+segmented lists and the dense-mask oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from multics_amd import metadata as M
+from oracle.masks import FullTopology, inactive_local_rows, mask_rows
+from tests import golden_io as G
+from tests.gpu_util import expand_tiles, need_gpu, say
+
+pytestmark = pytest.mark.gpu
+SEG_FIELDS = ("prog_qbase", "prog_nq", "prog_seg", "kv_index", "kv_count")
+TILED_FIELDS = ("prog_qbase", "prog_nq", "prog_seg", "kv_index", "kv_valid", "kv_count")
+
+
+def _seg_call(inp, return_tiles=False):
+    return M._build_metadata(
+        device="cuda", P=inp["P"], N=inp["N"], L=inp["L"], KL=inp["KL"], KG=inp["KG"],
+        n_frames=inp["n_frames"], n_block=inp["n_block"], local_attn=inp["local_attn"],
+        agent_frame_lists=inp["agent_frames"], local_frame_lists=inp["local_frames"],
+        global_frame_list=inp["global_frames"], local_active_frames=inp["local_active"],
+        labels=inp["labels"], q_active=inp["q_active"], direct_player=inp["direct"],
+        block_m=inp["block_m"], membership=inp["membership"], global_only=inp["global_only"],
+        hier_no_local_hub=inp["no_local"], return_tiles=return_tiles)
+
+
+@pytest.mark.parametrize("name", G.cases("seg"))
+def test_segmented_metadata_bit_exact(name):
+    need_gpu()
+    say("segmented metadata", name)
+    inp = G.inputs("seg", name)
+    M.clear_metadata_cache()
+    out = _seg_call(inp, return_tiles=True)
+    torch.cuda.synchronize()
+    for f, val in zip(SEG_FIELDS, out[:5]):
+        G.assert_same(f"seg/{name}/{f}", val.cpu().numpy())
+    assert out[5] == G.scalar(f"seg/{name}/logical_pairs")
+    # the attention tile list holds exactly the same key set per query row
+    kv_index, kv_count = out[3].cpu().numpy(), out[4].cpu().numpy()
+    qb, nq, sg = (x.cpu().numpy() for x in out[:3])
+    rows = expand_tiles(out[6])
+    for base, n, s in zip(qb, nq, sg):
+        keys = set(kv_index[s, :kv_count[s]].tolist())
+        for q in range(base, base + n):
+            assert rows[q] == keys, (name, q)
+
+
+@pytest.mark.parametrize("name", G.cases("tc"))
+def test_tiled_cached_layout_bit_exact(name):
+    need_gpu()
+    say("tiled cached layout", name)
+    inp = G.inputs("tc", name)
+    M.clear_hier_tiled_layout_cache()
+    lay = M.build_hier_tiled_cached_layout(
+        device="cuda", P=inp["P"], N=inp["N"], L=inp["L"], KL=inp["KL"], KG=inp["KG"],
+        n_frames=inp["n_frames"], n_block=inp["n_block"], local_attn=inp["local_attn"],
+        agent_frame_lists=inp["agent_frames"], local_frame_lists=inp["local_frames"],
+        global_frame_list=inp["global_frames"], local_active_frames=inp["local_active"],
+        labels=inp["labels"], q_active=inp["q_active"], direct_player=inp["direct"])
+    torch.cuda.synchronize()
+    for f in TILED_FIELDS:
+        G.assert_same(f"tc/{name}/{f}", getattr(lay, f).cpu().numpy())
+    for f in ("logical_slots", "physical_slots", "dense_slots"):
+        assert getattr(lay, f) == G.scalar(f"tc/{name}/{f}"), f
+
+
+@pytest.mark.parametrize("name", G.cases("tf"))
+def test_tiled_full_sequence_layouts_bit_exact(name):
+    need_gpu()
+    say("tiled full-sequence layouts", name)
+    inp = G.inputs("tf", name)
+    M.clear_hier_tiled_layout_cache()
+    lays = M.build_hier_tiled_full_sequence_layouts(
+        device="cuda", num_players=inp["P"], num_frames=inp["T"], num_patches=inp["L"],
+        num_groups=inp["N"], num_local_hub_tokens=inp["KL"], num_global_hub_tokens=inp["KG"],
+        num_frame_per_block=inp["n"], local_attn_size=inp["window"],
+        group_labels=torch.tensor(inp["labels"]), active_group=torch.tensor(inp["active"]),
+        direct_player=inp["direct"])
+    torch.cuda.synchronize()
+    assert len(lays) == G.scalar(f"tf/{name}/num_blocks")
+    for b, lay in enumerate(lays):
+        for f in TILED_FIELDS:
+            G.assert_same(f"tf/{name}/{b}/{f}", getattr(lay, f).cpu().numpy())
+        for f in ("logical_slots", "physical_slots", "dense_slots"):
+            assert getattr(lay, f) == G.scalar(f"tf/{name}/{b}/{f}"), f
+    if inp["T"] * inp["L"] * inp["P"] <= 4096:
+        topo = FullTopology(inp["P"], inp["T"], inp["L"], inp["N"], inp["KL"], inp["KG"], inp["n"],
+                            inp["window"], inp["direct"], labels=np.array(inp["labels"]),
+                            active=np.array(inp["active"]))
+        m = mask_rows(topo)
+        dead = inactive_local_rows(topo)
+        rows = expand_tiles(lays[0].tiles)
+        assert len(rows) == topo.S
+        for q in range(topo.S):
+            exp = set() if dead[q] else set(np.nonzero(m[q])[0].tolist())
+            assert rows[q] == exp, (name, q)
+
+
+def test_dynamic_membership_tile_list_matches_dense_mask():
+    """Per-frame membership (groups change inside a block), full sequence."""
+    need_gpu()
+    rng = np.random.default_rng(3)
+    P, T, L, N, KL, KG, n, W = 5, 6, 3, 3, 2, 2, 3, 4
+    mem = rng.random((T, N, P)) < 0.4
+    go = ~mem.any(1) & (rng.random((T, P)) < 0.7)
+    for direct in (False, True):
+        say("dynamic membership tile list, direct", direct)
+        topo = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                        direct=direct, membership=mem, global_only=go)
+        tiles = M.build(topo, "cuda").tiles
+        torch.cuda.synchronize()
+        ft = FullTopology(P, T, L, N, KL, KG, n, W, direct, membership=mem, global_only=go)
+        m = mask_rows(ft)
+        dead = inactive_local_rows(ft)
+        rows = expand_tiles(tiles)
+        assert len(rows) == ft.S
+        for q in range(ft.S):
+            exp = set() if dead[q] else set(np.nonzero(m[q])[0].tolist())
+            assert rows[q] == exp, q

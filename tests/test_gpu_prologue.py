@@ -1,0 +1,60 @@
+"""Fused camera + RMSNorm + RoPE prologue against the fp32/f64 oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from multics_amd.kernels import qkv_prologue
+from oracle import attention as OA
+from tests.gpu_util import err_stats, need_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _freqs(P, T, h, w, KG_total):
+    bands = OA.rerope_bands(128)
+    verts = OA.simplex_vertices(10, 32)
+    agent = torch.cat([OA.player_freqs(bands, T, h, w, verts, p) for p in range(P)], 0)
+    return torch.cat([agent, OA.hub_freqs(bands, T, KG_total)], 0)
+
+
+@pytest.mark.parametrize("camera", [False, True])
+@pytest.mark.parametrize("layout", ["shd", "hsd"])
+def test_prologue_matches_oracle(camera, layout):
+    need_gpu()
+    say("prologue camera", camera, layout)
+    P, T, h, w, H, D = 2, 3, 4, 5, 4, 128
+    K_total = 2 * 5 + 6
+    S = P * T * h * w + T * K_total
+    dim = H * D
+    g = torch.Generator().manual_seed(5)
+    qx = (torch.randn(S, dim, generator=g) * 0.7).to(torch.bfloat16)
+    kx = (torch.randn(S, dim, generator=g) * 0.7).to(torch.bfloat16)
+    vx = torch.randn(S, dim, generator=g).to(torch.bfloat16)
+    wq = (1 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16)
+    wk = (1 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16)
+    freqs = _freqs(P, T, h, w, K_total)
+    cam = wcq = wck = None
+    if camera:
+        cam = torch.zeros(S, 12)
+        cam[:P * T * h * w] = torch.randn(P * T * h * w, 12, generator=g)
+        cam = cam.to(torch.bfloat16)
+        wcq = (0.05 * torch.randn(dim, 12, generator=g)).to(torch.bfloat16)
+        wck = (0.05 * torch.randn(dim, 12, generator=g)).to(torch.bfloat16)
+    dev = "cuda"
+    q, k, v = qkv_prologue(
+        qx.to(dev), kx.to(dev), vx.to(dev), norm_q_w=wq.to(dev), norm_k_w=wk.to(dev),
+        rope_cos=freqs[:, 0].real.float().to(dev), rope_sin=freqs[:, 0].imag.float().to(dev),
+        num_heads=H, eps=1e-6, cam=None if cam is None else cam.to(dev),
+        w_cam_q=None if wcq is None else wcq.to(dev), w_cam_k=None if wck is None else wck.to(dev),
+        out_layout=layout)
+    torch.cuda.synchronize()
+    rq, rk = OA.project_qk(qx, kx, norm_q_w=wq, norm_k_w=wk, freqs=freqs, num_heads=H, eps=1e-6,
+                           cam=cam, w_cam_q=wcq, w_cam_k=wck)
+    for got, ref in ((q, rq), (k, rk)):
+        got = got.reshape(S, dim)
+        mx, mn = err_stats(got, ref)
+        same = (got.float().cpu() == ref).float().mean().item()
+        say(f"  max-abs {mx:.3e} mean-abs {mn:.3e} identical {same:.5f}")
+        assert mx <= 2e-2 and mn <= 2e-4 and same > 0.99
+    assert torch.equal(v.reshape(S, dim).cpu(), vx)
