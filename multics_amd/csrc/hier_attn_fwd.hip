@@ -8,19 +8,23 @@
 // visited; there is no dense S x S mask anywhere.
 //
 // Per workgroup: 4 waves x 32 query rows.  Keys stream through LDS in tiles of
-// 64 gathered rows, double buffered: K row-major, V transposed (d-major) with
-// the keys of every 16-key group permuted so that the P operand of P.V can be
-// fed straight from the registers of the QK^T result.
+// 64 gathered rows, double buffered; K and V tiles share one row-major layout
+// (four threads move one 256-byte key row with 16-byte loads and stores).
 //
 // Math per wave and tile (v_mfma_f32_32x32x16_bf16):
 //   S^T[key, q]  = K[key, :] . Q[q, :]           2 key blocks x D/16 MFMAs
 //   online softmax over keys: max / sum are in-register over the lane's 16
 //   keys per block plus one swap with lane^32 (v_permlane32_swap)
 //   O^T[d, q]   += V^T[d, key] . P^T[key, q]      D/32 x 4 MFMAs
+// The P^T operand comes straight from the S^T registers; the matching V^T
+// operand is read with ds_read_b64_tr_b16 (a 4 x 16 block of 16-bit values,
+// transposed across each 16-lane group), two reads per MFMA.
 // fp32 m / l / O, P rounded to bf16 before P.V, exp2 with the log2(e)-scaled
 // softmax scale folded into one FMA -- the numerics of the reference kernels
-// (hier_tiled_attention.py:112-143).  Rows with no visible key output 0
-// (hier_segmented_attention.py:104-109).
+// (hier_tiled_attention.py:112-143).  The running max is refreshed lazily: the
+// accumulators are rescaled only when a row's max grows by more than 2^8 in
+// exp2 units, which leaves O / l unchanged and keeps P below 256.  Rows with
+// no visible key output 0 (hier_segmented_attention.py:104-109).
 #include "hier_common.h"
 
 namespace {
@@ -29,26 +33,33 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRows = 32 * kWaves;     // query rows per work item
 constexpr int kKT = 64;                // keys per LDS tile
-constexpr int kVPitch = kKT + 8;       // bf16 per V^T row (padded)
+constexpr float kRescaleLog2 = 8.0f;   // lazy-rescale threshold (exp2 units)
+
+// LDS row pitches (bf16).  K rows are read 16 rows per cycle at one column
+// (the S^T A operand): consecutive rows shift by 4 banks.  V rows are read
+// four keys x four 8-byte chunks per 16-lane group (transposed reads) and are
+// written eight keys x two adjacent 16-byte chunks per group: consecutive rows
+// shift by 8 (D=128) or 40 (D=64) banks.  All three patterns are free of bank
+// conflicts on a 64-bank LDS.
+template <int D>
+struct Tile {
+  static constexpr int kPitchK = D == 128 ? 136 : 72;
+  static constexpr int kPitchV = D == 128 ? 144 : 80;
+};
 
 template <int D>
 struct Smem {
-  static constexpr int kPitch = D + 8;             // bf16 per K row (padded)
-  uint16_t k[2][kKT * kPitch];
-  uint16_t vt[2][D * kVPitch];
+  uint16_t k[2][kKT * Tile<D>::kPitchK];
+  uint16_t v[2][kKT * Tile<D>::kPitchV];
   uint32_t km[2][kKT];
 };
-
-// Position of key x (0..15) of a 16-key group inside a V^T row: the 8 keys that
-// one half-wave multiplies in P.V become contiguous (a 16-byte LDS read).
-__device__ __forceinline__ int vt_pos(int x) {
-  return ((x >> 2) & 1) * 8 + (x >> 3) * 4 + (x & 3);
-}
 
 __device__ __forceinline__ float pair_max(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -69,11 +80,28 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);  // round to nearest even
 }
 
+// V^T operand of O^T += V^T P^T for rows d = d0 + (lane & 15) of this lane's
+// 16-lane group: two transposed reads of 4 keys each (keys 16kc + 4h + r and
+// 16kc + 8 + 4h + r, r = 0..3, h = lane >> 5) -- the key order of the P^T
+// operand taken from the S^T accumulator.
+template <int KP>
+__device__ __forceinline__ bf16x8 load_vt(const uint16_t* vbuf, int kc, int d0, int lane) {
+  const int h = lane >> 5, i = lane & 15;
+  const int key = 16 * kc + 4 * h + (i >> 2);
+  const uint16_t* p0 = vbuf + key * KP + d0 + 4 * (i & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 8 * KP));
+  const s16x8 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, ab);
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, int total) {
   constexpr int NC = D / 16;   // d-chunks of QK^T
   constexpr int NDB = D / 32;  // d-blocks of O^T
-  constexpr int KP = Smem<D>::kPitch;
+  constexpr int KPK = Tile<D>::kPitchK;
+  constexpr int KPV = Tile<D>::kPitchV;
+  constexpr int NV = D / 32;   // 16-byte vectors per thread per K (or V) tile
   __shared__ __align__(16) Smem<D> sm;
 
   // XCD-aware mapping: consecutive logical items land on the same XCD (the
@@ -112,86 +140,82 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
     for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
   }
 
-  // loader mapping: 32 key pairs x 8 d-groups; thread (pair, dg) moves keys
-  // 2*pair and 2*pair+1, elements [dg*D/8, (dg+1)*D/8)
-  constexpr int DG = D / 8;              // elements per d-group
-  constexpr int NV = DG / 8;             // 16-byte vectors per key per thread
-  const int pair = tid & 31, dg = tid >> 5;
+  // loaders (every thread moves NV 16-byte vectors of K and of V per tile):
+  //  K: key = tid % 64, elements [q*D/4, (q+1)*D/4) with q = tid / 64
+  //  V: 16-lane group m = tid / 16 stores keys 8*(m%8) + i/2 (i = tid % 16),
+  //     16-byte chunk 2*((m/8)*NV + e) + i%2 for vector e
+  const int kkey = tid & 63, kq = tid >> 6;
+  const int vgrp = tid >> 4, vi = tid & 15;
+  const int vkey = 8 * (vgrp & 7) + (vi >> 1);
   const int64_t k_head = (int64_t)head * a.k_sh, v_head = (int64_t)head * a.v_sh;
-
-  u32x4 kreg[2][NV], vreg[2][NV];
+  u32x4 kreg[NV], vreg[NV];
   uint32_t mreg = 0;
   const int ntiles = kv_cnt / kKT;
+  int kidx = 0, vidx = 0;   // K/V pool rows of the next tile to fetch
 
-  auto gload = [&](int t) {
+  auto fetch_idx = [&](int t) {   // t < ntiles
     const int base = kv_off + t * kKT;
-    const int i0 = a.tile_kv_idx[base + 2 * pair];
-    const int i1 = a.tile_kv_idx[base + 2 * pair + 1];
-    const uint16_t* k0 = a.k + (int64_t)i0 * a.k_ss + k_head + dg * DG;
-    const uint16_t* k1 = a.k + (int64_t)i1 * a.k_ss + k_head + dg * DG;
-    const uint16_t* v0 = a.v + (int64_t)i0 * a.v_ss + v_head + dg * DG;
-    const uint16_t* v1 = a.v + (int64_t)i1 * a.v_ss + v_head + dg * DG;
-#pragma unroll
-    for (int e = 0; e < NV; ++e) {
-      kreg[0][e] = *reinterpret_cast<const u32x4*>(k0 + 8 * e);
-      kreg[1][e] = *reinterpret_cast<const u32x4*>(k1 + 8 * e);
-      vreg[0][e] = *reinterpret_cast<const u32x4*>(v0 + 8 * e);
-      vreg[1][e] = *reinterpret_cast<const u32x4*>(v1 + 8 * e);
-    }
-    if (tid < kKT) mreg = a.tile_kv_mask[base + tid];
+    kidx = a.tile_kv_idx[base + kkey];
+    vidx = a.tile_kv_idx[base + vkey];
   };
-
-  auto lstore = [&](int buf) {
-    const int key0 = 2 * pair;
+  auto gload = [&](int t) {       // uses kidx / vidx fetched for tile t
+    const uint16_t* kp = a.k + (int64_t)kidx * a.k_ss + k_head + kq * (D / 4);
+    const uint16_t* vp = a.v + (int64_t)vidx * a.v_ss + v_head;
 #pragma unroll
     for (int e = 0; e < NV; ++e) {
-      *reinterpret_cast<u32x4*>(&sm.k[buf][key0 * KP + dg * DG + 8 * e]) = kreg[0][e];
-      *reinterpret_cast<u32x4*>(&sm.k[buf][(key0 + 1) * KP + dg * DG + 8 * e]) = kreg[1][e];
+      kreg[e] = *reinterpret_cast<const u32x4*>(kp + 8 * e);
+      const int chunk = 2 * ((vgrp >> 3) * NV + e) + (vi & 1);
+      vreg[e] = *reinterpret_cast<const u32x4*>(vp + 8 * chunk);
     }
-    // V^T: word (keys key0, key0+1) of row d; key0 even so both share a word
-    const int pos = (key0 & ~15) + vt_pos(key0 & 15);
+    if (tid < kKT) mreg = a.tile_kv_mask[kv_off + t * kKT + tid];
+  };
+  auto lstore = [&](int buf) {
+    uint16_t* kd = &sm.k[buf][kkey * KPK + kq * (D / 4)];
+    uint16_t* vd = &sm.v[buf][vkey * KPV];
 #pragma unroll
     for (int e = 0; e < NV; ++e) {
-      const u32x4 w0 = vreg[0][e], w1 = vreg[1][e];
-#pragma unroll
-      for (int h2 = 0; h2 < 4; ++h2) {
-        const int d = dg * DG + 8 * e + 2 * h2;
-        const uint32_t lo = (w0[h2] & 0xffffu) | (w1[h2] << 16);
-        const uint32_t hi = (w0[h2] >> 16) | (w1[h2] & 0xffff0000u);
-        *reinterpret_cast<uint32_t*>(&sm.vt[buf][d * kVPitch + pos]) = lo;
-        *reinterpret_cast<uint32_t*>(&sm.vt[buf][(d + 1) * kVPitch + pos]) = hi;
-      }
+      *reinterpret_cast<u32x4*>(kd + 8 * e) = kreg[e];
+      const int chunk = 2 * ((vgrp >> 3) * NV + e) + (vi & 1);
+      *reinterpret_cast<u32x4*>(vd + 8 * chunk) = vreg[e];
     }
     if (tid < kKT) sm.km[buf][tid] = mreg;
   };
 
   const float c2 = a.scale * 1.4426950408889634f;  // softmax scale * log2(e)
-  float m_run = -INFINITY, l_run = 0.f;
+  const float thr = kRescaleLog2 / c2;             // lazy-rescale margin in score units
+  float m_ref = -INFINITY, l_run = 0.f;
   f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  const f32x16 zero = {};
 
   if (ntiles > 0) {
+    fetch_idx(0);
     gload(0);
     lstore(0);
+    fetch_idx(ntiles > 1 ? 1 : 0);
   }
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
+    // Prefetch tile t+1 unconditionally (the last iteration re-reads tile t):
+    // a conditional load here makes the compiler wait on it before the MFMAs.
+    const int tn = t + 1 < ntiles ? t + 1 : t;
+    gload(tn);
+    fetch_idx(t + 2 < ntiles ? t + 2 : tn);
     if (wave_active) {
       // ---- S^T = K Q^T -------------------------------------------------------
       f32x16 s[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
+        const uint16_t* kp = &sm.k[buf][(kb * 32 + col) * KPK + 8 * half];
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            *reinterpret_cast<const bf16x8*>(kp), qf[0], zero, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-        const uint16_t* kp = &sm.k[buf][(kb * 32 + col) * KP + 8 * half];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
+        for (int c = 1; c < NC; ++c) {
           bf16x8 kf = *reinterpret_cast<const bf16x8*>(kp + 16 * c);
           s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], s[kb], 0, 0, 0);
         }
@@ -209,40 +233,42 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
               if (!((mk[e] >> qframe) & 1u)) s[kb][4 * g4 + e] = -INFINITY;
           }
       }
-      // ---- online softmax -----------------------------------------------------
-      float mx = s[0][0];
+      // ---- online softmax (lazy rescale) ----------------------------------------
+      float mx = fmaxf(s[0][0], s[0][1]);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int r = 2; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[0][r], s[0][r + 1]));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[1][r], s[1][r + 1]));
       mx = pair_max(mx);
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c2);
-      const float nb = -m_use * c2;
-      m_run = m_new;
-      float psum = 0.f;
+      if (__ballot(mx > m_ref + thr) != 0) {
+        const float m_new = fmaxf(m_ref, mx);
+        const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_ref - m_new) * c2);
+        m_ref = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      }
+      const float nb = (m_ref == -INFINITY) ? 0.f : -m_ref * c2;
+      float ps0 = 0.f, ps1 = 0.f;
       bf16x8 pk[4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], c2, nb));
-          psum += p;
+          if (r & 1) ps1 += p; else ps0 += p;
           pk[kb * 2 + (r >> 3)][r & 7] = (__bf16)p;
         }
-      l_run = l_run * alpha + psum;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      l_run += ps0 + ps1;
       // ---- O^T += V^T P^T ------------------------------------------------------
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const uint16_t* vp = &sm.vt[buf][(db * 32 + col) * kVPitch + 8 * half];
+        const int d0 = db * 32 + 16 * ((lane >> 4) & 1);
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
-          bf16x8 vf = *reinterpret_cast<const bf16x8*>(vp + 16 * kc);
+          const bf16x8 vf = load_vt<KPV>(sm.v[buf], kc, d0, lane);
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pk[kc], o[db], 0, 0, 0);
         }
       }
@@ -267,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
         *reinterpret_cast<u32x2*>(op + d0) = w;
       }
     if (a.lse && half == 0) {
-      const float lse = l_tot > 0.f ? m_run * a.scale + __logf(l_tot) : -INFINITY;
+      const float lse = l_tot > 0.f ? m_ref * a.scale + __logf(l_tot) : -INFINITY;
       a.lse[(int64_t)head * a.lse_stride_h + qtok] = lse;
     }
   }

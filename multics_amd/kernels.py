@@ -116,8 +116,8 @@ def hierarchical_tiled_full_sequence_attention(*, roped_q: torch.Tensor, roped_k
         hier_attention_forward(roped_q, roped_k, value, tiles, out)
     else:
         for b in blocks:
-            hier_attention_forward(roped_q, roped_k, value, tiles, out,
-                                   item_range=tiles.item_ranges[b])
+            for rng in tiles.item_ranges[b]:
+                hier_attention_forward(roped_q, roped_k, value, tiles, out, item_range=rng)
     return out.reshape(batch, seq_len, heads * head_dim)
 
 

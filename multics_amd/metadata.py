@@ -54,7 +54,7 @@ class TileList:
     kv_mask: torch.Tensor        # [n_keys] int32 (uint32 bits)
     blk_and: torch.Tensor        # [n_keys / 64] int32 (uint32 bits)
     n_items: int
-    item_ranges: tuple           # per block: (first item, end item)
+    item_ranges: tuple           # per block: ((first item, end item) per stream, ...)
     logical_pairs: int           # useful (q, k) pairs (FLOP accounting)
     key_extent: int = 0          # 1 + largest K/V row index any key can address
     row_extent: int = 0          # 1 + largest Q/O row index any item can address
@@ -401,14 +401,25 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     n_keys = int(tile_off[-1])
     rows = np.array([[n * _qlen(topo, s) for s in range(NS)] for _ in range(B)], dtype=np.int64)
     nit = -(-rows // rows_per_item)
-    item_off = np.concatenate([[0], np.cumsum(nit.reshape(-1))])
-    n_items = int(item_off[-1])
+    # Work-item order: stream-major (local hubs, players, global), then block.
+    # Consecutive items of one player cover consecutive temporal blocks, whose
+    # key windows overlap in all but n frames, so the workgroups an XCD runs
+    # together share most of their K/V lines in that XCD's L2; the longest
+    # key lists (local hubs) start first.
+    order = [s for s in range(P, P + N)] + list(range(P)) + [P + N]
+    item_start = np.zeros((B, NS), dtype=np.int64)
+    cursor = 0
+    for s in order:
+        for b in range(B):
+            item_start[b, s] = cursor
+            cursor += int(nit[b, s])
+    n_items = cursor
     kv_idx = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
     kv_mask = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
     blk_and = torch.empty(max(n_keys // TILE_KEYS, 1), dtype=torch.int32, device=dev)
     items = torch.empty((max(n_items, 1), 8), dtype=torch.int32, device=dev)
     out.tile_kv_off = dbuf(tile_off[:-1]).data_ptr()
-    out.tile_item_off = dbuf(item_off[:-1], torch.int32).data_ptr()
+    out.tile_item_off = dbuf(item_start.reshape(-1), torch.int32).data_ptr()
     out.rows_per_item = rows_per_item
     out.tile_kv_idx, out.tile_kv_mask = kv_idx.data_ptr(), kv_mask.data_ptr()
     out.tile_blk_and, out.tile_items = blk_and.data_ptr(), items.data_ptr()
@@ -478,7 +489,8 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
 
     _capi.call("hier_meta_build", C.byref(t), C.byref(out), stream)
 
-    ranges = tuple((int(item_off[b * NS]), int(item_off[(b + 1) * NS])) for b in range(B))
+    ranges = tuple(tuple((int(item_start[b, s]), int(item_start[b, s] + nit[b, s]))
+                         for s in range(NS) if nit[b, s] > 0) for b in range(B))
     key_ext = 0
     for b in range(B):
         for rows_, w in ((topo.tile_agent_base[b], topo.L), (topo.tile_local_base[b], topo.KL),
