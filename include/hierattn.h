@@ -170,6 +170,8 @@ typedef struct HierFwdArgs {
   int32_t H, D;                    /* heads, head dim (must be 128)            */
   int32_t n_items;                 /* work items (tile_items rows)             */
   float scale;                     /* softmax scale (1/sqrt(D))                */
+  int32_t kv_rows;                 /* rows addressable in k / v (> every key index) */
+  int32_t reserved;                /* must be 0                                */
   const uint16_t* q;               /* bf16, element (s,h,d) at s*q_ss + h*q_sh + d */
   const uint16_t* k;
   const uint16_t* v;

@@ -1,7 +1,7 @@
 """ctypes binding of the C ABI in ``include/hierattn.h``.
 
 The library is loaded from ``multics_amd/_lib/libhierattn.so`` (built in tree
-by ``multics_amd.build``).  There is no fallback: when the library is missing
+by ``multics_amd.build``), or from the file named by ``HIERATTN_LIB``.  There is no fallback: when the library is missing
 the import of a compute entry point raises.  Error codes map back to the
 exception types the reference raises for the same conditions
 (multics/models/kernels/hier_segmented_attention.py:425-431 NotImplementedError,
@@ -13,10 +13,12 @@ multics/models/kernels/hier_packed_attention.py:54-64 AssertionError).
 from __future__ import annotations
 
 import ctypes as C
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libhierattn.so"
+LIB_PATH = Path(os.environ.get("HIERATTN_LIB") or
+                Path(__file__).resolve().parent / "_lib" / "libhierattn.so")
 
 HIER_OK, HIER_EINVAL, HIER_EUNSUPPORTED, HIER_ELAUNCH, HIER_EINTERNAL = 0, -1, -2, -3, -4
 
@@ -63,7 +65,8 @@ class HierPrologueArgs(C.Structure):
 
 
 class HierFwdArgs(C.Structure):
-    _fields_ = [("H", i32), ("D", i32), ("n_items", i32), ("scale", f32)] + \
+    _fields_ = [("H", i32), ("D", i32), ("n_items", i32), ("scale", f32), ("kv_rows", i32),
+                ("reserved", i32)] + \
                [(n, vp) for n in ("q", "k", "v", "o", "lse")] + \
                [(n, i64) for n in ("q_ss", "q_sh", "k_ss", "k_sh", "v_ss", "v_sh", "o_ss", "o_sh",
                                    "lse_stride_h")] + \

@@ -4,7 +4,9 @@ One ``hipcc`` invocation over ``multics_amd/csrc/*.hip``; no torch extension,
 no CMake.  Packed-FP32 instruction selection (v_pk_*_f32) is disabled for
 every device translation unit because some of its forms have produced silent
 wrong results on the target machines; the host pass warns that it does not
-know the feature, which is harmless.
+know the feature, which is harmless.  ``-fno-honor-nans`` lets fmax compile to
+plain v_max / v_max3 without NaN canonicalisation (infinities are still
+honoured: masked scores are -inf).
 """
 
 from __future__ import annotations
@@ -35,6 +37,7 @@ def build(verbose: bool = False) -> Path:
     sources = sorted(str(p) for p in CSRC.glob("*.hip"))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+           "-fno-honor-nans",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
            f"-I{ROOT / 'include'}", f"-I{CSRC}", *sources, "-o", str(tmp)]
     if verbose:

@@ -7,59 +7,91 @@
 // per-key bitmask saying which query frames may see it.  Only listed keys are
 // visited; there is no dense S x S mask anywhere.
 //
-// Per workgroup: 4 waves x 32 query rows.  Keys stream through LDS in tiles of
-// 64 gathered rows, double buffered; K and V tiles share one row-major layout
-// (four threads move one 256-byte key row with 16-byte loads and stores).
-//
-// Math per wave and tile (v_mfma_f32_32x32x16_bf16):
-//   S^T[key, q]  = K[key, :] . Q[q, :]           2 key blocks x D/16 MFMAs
-//   online softmax over keys: max / sum are in-register over the lane's 16
-//   keys per block plus one swap with lane^32 (v_permlane32_swap)
-//   O^T[d, q]   += V^T[d, key] . P^T[key, q]      D/32 x 4 MFMAs
+// Math (v_mfma_f32_32x32x16_bf16), per 32-row sub-block and 32-key block:
+//   S^T[key, q]  = K[key, :] . Q[q, :]            D/16 MFMAs
+//   online softmax over keys: each lane owns one query and 16 keys per block;
+//   max / sum are in-register plus one swap with lane^32 (v_permlane32_swap)
+//   O^T[d, q]   += V^T[d, key] . P^T[key, q]       D/32 x 2 MFMAs
 // The P^T operand comes straight from the S^T registers; the matching V^T
-// operand is read with ds_read_b64_tr_b16 (a 4 x 16 block of 16-bit values,
-// transposed across each 16-lane group), two reads per MFMA.
-// fp32 m / l / O, P rounded to bf16 before P.V, exp2 with the log2(e)-scaled
-// softmax scale folded into one FMA -- the numerics of the reference kernels
-// (hier_tiled_attention.py:112-143).  The running max is refreshed lazily: the
-// accumulators are rescaled only when a row's max grows by more than 2^8 in
-// exp2 units, which leaves O / l unchanged and keeps P below 256.  Rows with
-// no visible key output 0 (hier_segmented_attention.py:104-109).
+// operand is read with ds_read_b64_tr_b16 (each 16-lane group reads a 4 x 16
+// block and lane i receives column i), two reads per MFMA.  fp32 m / l / O, P
+// rounded to bf16 before P.V, exp2 with the log2(e)-scaled softmax scale folded
+// into one FMA -- the numerics of the reference kernels
+// (hier_tiled_attention.py:112-143); the row sum l adds the bf16-rounded P
+// (v_dot2_f32_bf16), i.e. exactly the weights that multiply V.  The running max
+// is refreshed lazily: O and l are rescaled only when a row's max grows by more
+// than 2^8 in exp2 units.  Rows with no visible key output 0
+// (hier_segmented_attention.py:104-109).
+//
+// Workgroup = 4 waves x 32 query rows (128 rows per work item), two
+// workgroups per CU.  Keys stream through LDS in 64-key tiles that the waves
+// copy with global_load_lds_dwordx4 (HBM/L2 -> LDS, no VGPR staging).  Each
+// wave runs a three-stage software pipeline over 32-key blocks whose stages
+// are independent within one step, so the softmax VALU work overlaps both
+// matrix products:
+//     step j:  QK(j+2)  ||  softmax(j+1)  ||  PV(j)
+// While the two blocks of tile t are multiplied by V, K tile t+2 (with its
+// masks) and V tile t+1 are in flight; two K, two V and two mask stages fill
+// 65 KB of LDS per workgroup.
+//
+// LDS layout of a tile: key rows of 2*D bytes with no padding.  Key j of a
+// 16-key group sits in row NR*(j % NI) + j / NI of the group (NI = D/32 copy
+// instructions per wave, NR = 64 lanes / (D/8) chunks = rows per instruction),
+// so each lane copies NI consecutive keys of one row slot.  16-byte chunks are
+// XOR-swizzled per key (K: every 16 consecutive keys of one chunk column land
+// in 16 different bank groups; V: the 4 rows x 4 chunks of one transposed read
+// land in 16 different bank groups).
 #include "hier_common.h"
 
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kKT = 64;                // keys per LDS tile
+constexpr int kSlab = 64;              // keys per LDS tile
 constexpr float kRescaleLog2 = 8.0f;   // lazy-rescale threshold (exp2 units)
 
-// LDS row pitches (bf16).  K rows are read 16 rows per cycle at one column
-// (the S^T A operand): consecutive rows shift by 4 banks.  V rows are read
-// four keys x four 8-byte chunks per 16-lane group (transposed reads) and are
-// written eight keys x two adjacent 16-byte chunks per group: consecutive rows
-// shift by 8 (D=128) or 40 (D=64) banks.  All three patterns are free of bank
-// conflicts on a 64-bank LDS.
 template <int D>
-struct Tile {
-  static constexpr int kPitchK = D == 128 ? 136 : 72;
-  static constexpr int kPitchV = D == 128 ? 144 : 80;
+struct Geo {
+  static constexpr int ROWB = 2 * D;                // bytes per key row
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int NI = D / 32;                 // copy instructions per wave per tile
+  static constexpr int NR = 64 / CPR;               // rows per copy instruction
+  static constexpr int TILEB = kSlab * ROWB;
+  static constexpr int MBYTES = kSlab * 4;
+  static constexpr int KOFF = 0;
+  static constexpr int VOFF = 2 * TILEB;
+  static constexpr int MOFF = 4 * TILEB;
+  static constexpr int LDS = 4 * TILEB + 2 * MBYTES;
+  static constexpr int NC = D / 16;                 // d-chunks of QK^T
+  static constexpr int NDB = D / 32;                // d-blocks of O^T
+  static_assert(NI * NR == 16, "a wave copies 16 keys per tile");
 };
 
+// Row of key `key` inside its tile.
 template <int D>
-struct Smem {
-  uint16_t k[2][kKT * Tile<D>::kPitchK];
-  uint16_t v[2][kKT * Tile<D>::kPitchV];
-  uint32_t km[2][kKT];
-};
+__device__ __forceinline__ int prow(int key) {
+  const int j = key & 15;
+  return (key & ~15) + Geo<D>::NR * (j % Geo<D>::NI) + j / Geo<D>::NI;
+}
+// Chunk swizzles (XOR masks on the 16-byte chunk index of a row).
+template <int D>
+__device__ __forceinline__ int swz_k(int key) {
+  return D == 128 ? (key & 15) : ((key & 1) | ((key >> 1) & 6));
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int key) {
+  return D == 128 ? 4 * (key & 3) : 4 * (key & 1);
+}
 
 __device__ __forceinline__ float pair_max(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -69,233 +101,428 @@ __device__ __forceinline__ float pair_sum(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-
 __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) v |= __shfl_xor(v, d, 64);
   return v;
 }
-
 __device__ __forceinline__ uint16_t f2bf(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);  // round to nearest even
 }
 
-// V^T operand of O^T += V^T P^T for rows d = d0 + (lane & 15) of this lane's
-// 16-lane group: two transposed reads of 4 keys each (keys 16kc + 4h + r and
-// 16kc + 8 + 4h + r, r = 0..3, h = lane >> 5) -- the key order of the P^T
-// operand taken from the S^T accumulator.
-template <int KP>
-__device__ __forceinline__ bf16x8 load_vt(const uint16_t* vbuf, int kc, int d0, int lane) {
-  const int h = lane >> 5, i = lane & 15;
-  const int key = 16 * kc + 4 * h + (i >> 2);
-  const uint16_t* p0 = vbuf + key * KP + d0 + 4 * (i & 3);
-  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
-  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 8 * KP));
-  const s16x8 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  return __builtin_bit_cast(bf16x8, ab);
+// ---- tile copies (global -> LDS) -------------------------------------------
+
+// Per-lane constants of the tile copies: the lane copies chunk pc of row slot
+// r for keys 16*wave + NI*r + e, e < NI.  With that key order the swizzled
+// chunk of copy e is (pk ^ e) for K and (pc ^ 4e) for V.
+template <int D>
+struct Copier {
+  uint32_t pk16, pc16;   // 16 * pk, 16 * pc
+  int idx_off;           // first key of the lane inside a tile
+  __device__ __forceinline__ void init(int wave, int lane) {
+    const int r = lane / Geo<D>::CPR, pc = lane % Geo<D>::CPR;
+    idx_off = 16 * wave + Geo<D>::NI * r;
+    const int pk = pc ^ (swz_k<D>(idx_off) & ~(Geo<D>::NI - 1));
+    pk16 = 16u * (uint32_t)pk;
+    pc16 = 16u * (uint32_t)pc;
+  }
+  __device__ __forceinline__ uint32_t add_k(int e) const { return pk16 ^ (16u * e); }
+  __device__ __forceinline__ uint32_t add_v(int e) const { return pc16 ^ (64u * e); }
+};
+
+template <int D>
+struct Idx {
+  int v[Geo<D>::NI];
+};
+
+template <int D>
+__device__ __forceinline__ Idx<D> load_idx(const int32_t* kv_idx, int tile, int idx_off) {
+  Idx<D> r;
+  const int32_t* p = kv_idx + tile * kSlab + idx_off;
+  if constexpr (Geo<D>::NI == 4) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r.v[e] = (int)w[e];
+  } else {
+    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) r.v[e] = (int)w[e];
+  }
+  return r;
+}
+
+// One operand tile: NI 16-byte copies per lane, 1 KB per wave instruction.
+// g points at head `head` of row 0 of K (IS_V false) or V.
+template <int D, bool IS_V>
+__device__ __forceinline__ void copy_tile(const char* g, uint32_t ss_bytes, const Copier<D>& cp,
+                                          const Idx<D>& ix, char* slot, int wave) {
+#pragma unroll
+  for (int e = 0; e < Geo<D>::NI; ++e) {
+    const uint32_t off = (uint32_t)ix.v[e] * ss_bytes + (IS_V ? cp.add_v(e) : cp.add_k(e));
+    __builtin_amdgcn_global_load_lds(
+        (gbl_void*)(g + off),
+        (lds_void*)(slot + (16 * wave + Geo<D>::NR * e) * Geo<D>::ROWB), 16, 0, 0);
+  }
+}
+
+// Visibility masks of one tile (one dword per key, natural key order).
+__device__ __forceinline__ void copy_masks(const uint32_t* m, char* slot, int lane) {
+  __builtin_amdgcn_global_load_lds((gbl_void*)(m + lane), (lds_void*)slot, 4, 0, 0);
+}
+
+__device__ __forceinline__ void wait_copies() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), other counters untouched
+}
+
+// ---- per-sub-block state and math ------------------------------------------
+
+template <int D>
+struct Rows {
+  bf16x8 q[Geo<D>::NC];
+  f32x16 o[Geo<D>::NDB];
+  float m, l, alpha;
+  int qtok, qframe;
+  bool valid;
+  uint32_t bits;   // OR over the sub-block's valid rows of 1 << query frame
+};
+
+template <int D>
+__device__ __forceinline__ void rows_init(Rows<D>& R, const HierFwdArgs& a, const int32_t* it,
+                                          int head, int rrel, int lane) {
+  const int qbase = it[0], qstride = it[1], qlen = it[2], row_start = it[3], row_count = it[4];
+  const int r = rrel + (lane & 31);
+  R.valid = r < row_count;
+  const int ri = row_start + (R.valid ? r : 0);
+  R.qframe = ri / qlen;
+  R.qtok = qbase + R.qframe * qstride + (ri - R.qframe * qlen);
+  R.bits = wave_or(R.valid ? (1u << R.qframe) : 0u);
+  const uint16_t* qp = a.q + (int64_t)R.qtok * a.q_ss + (int64_t)head * a.q_sh + 8 * (lane >> 5);
+#pragma unroll
+  for (int c = 0; c < Geo<D>::NC; ++c) R.q[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) R.o[db][i] = 0.f;
+  R.m = -INFINITY;
+  R.l = 0.f;
+  R.alpha = 1.f;
+}
+
+// Per-lane LDS byte offsets of the MFMA operand reads (tile-relative).
+template <int D>
+struct ReadAddr {
+  int k[Geo<D>::NC];     // K row of key (lane & 31), chunk (lane >> 5) + 2c
+  int v[Geo<D>::NDB];    // first transposed V read of d-block db, key chunk 0
+  __device__ __forceinline__ void init(int lane) {
+    const int kk = lane & 31;
+#pragma unroll
+    for (int c = 0; c < Geo<D>::NC; ++c)
+      k[c] = prow<D>(kk) * Geo<D>::ROWB + 16 * (((lane >> 5) + 2 * c) ^ swz_k<D>(kk));
+    const int i = lane & 15;
+    const int key = 4 * (lane >> 5) + (i >> 2);
+    const int q = 2 * ((lane >> 4) & 1) + ((i & 3) >> 1);
+#pragma unroll
+    for (int db = 0; db < Geo<D>::NDB; ++db)
+      v[db] = prow<D>(key) * Geo<D>::ROWB + 16 * ((4 * db + q) ^ swz_v<D>(key)) + 8 * (i & 1);
+  }
+};
+
+// S^T of 32-key block kb of a tile.
+template <int D>
+__device__ __forceinline__ f32x16 qk_block(const bf16x8* q, const char* kslot, const ReadAddr<D>& ra,
+                                           int kb) {
+  const char* base = kslot + kb * 32 * Geo<D>::ROWB;
+  const f32x16 zero = {};
+  f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+      *reinterpret_cast<const bf16x8*>(base + ra.k[0]), q[0], zero, 0, 0, 0);
+#pragma unroll
+  for (int c = 1; c < Geo<D>::NC; ++c)
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(base + ra.k[c]),
+                                                q[c], s, 0, 0, 0);
+  return s;
+}
+
+// Set the scores of block kb that the lane's query frame may not see to -inf.
+__device__ __forceinline__ void mask_block(f32x16& s, const char* mslot, int kb, int qframe,
+                                           int lane) {
+  const uint32_t* mk = reinterpret_cast<const uint32_t*>(mslot);
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[kb * 32 + 8 * g4 + 4 * (lane >> 5)]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t sel = (uint32_t)__builtin_amdgcn_sbfe((int)w[e], qframe, 1);
+      const uint32_t x = __float_as_uint(s[4 * g4 + e]);
+      s[4 * g4 + e] = __uint_as_float((x & sel) | (0xff800000u & ~sel));
+    }
+  }
+}
+
+// Online softmax of one 32-key block (branch-free).  Writes P (bf16) as the two
+// P^T operands of the block, updates m / l and R.alpha; returns whether any
+// lane of the wave needs its O rescaled by alpha before the next P.V.
+template <int D>
+__device__ __forceinline__ bool softmax_block(Rows<D>& R, const f32x16& s, bf16x8* p, float c2,
+                                              float thr) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[i], s[i + 1]));
+  mx = pair_max(mx);
+  const bool any = __ballot(mx > R.m + thr) != 0;
+  const float m_new = any ? fmaxf(R.m, mx) : R.m;
+  R.alpha = (m_new == R.m) ? 1.f : __builtin_amdgcn_exp2f((R.m - m_new) * c2);
+  R.m = m_new;
+  const float nb = (m_new == -INFINITY) ? 0.f : -m_new * c2;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    p[i >> 3][i & 7] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[i], c2, nb));
+  const bf16x2 one = {(__bf16)1.f, (__bf16)1.f};
+  float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    ps0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[c], p[c], 0, 1), one, ps0, false);
+    ps1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[c], p[c], 2, 3), one, ps1, false);
+    ps0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[c], p[c], 4, 5), one, ps0, false);
+    ps1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[c], p[c], 6, 7), one, ps1, false);
+  }
+  R.l = R.l * R.alpha + (ps0 + ps1);
+  return any;
+}
+
+template <int D>
+__device__ __forceinline__ void rescale(Rows<D>& R, float alpha) {
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) R.o[db][i] *= alpha;
+}
+
+// O^T += V^T P^T over the two 16-key chunks kc = 2kb, 2kb+1 of block kb.
+// Chunk kc holds keys 16kc + 4h + r and 16kc + 8 + 4h + r (h = lane >> 5,
+// r = 0..3): the key order of the P^T operand taken from the S^T registers.
+template <int D>
+__device__ __forceinline__ void pv_block(Rows<D>& R, const bf16x8* p, const char* vslot,
+                                         const ReadAddr<D>& ra, int kb) {
+  constexpr int HALF = (8 / Geo<D>::NI) * Geo<D>::ROWB;   // rows of keys +8
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int db = 0; db < Geo<D>::NDB; ++db) {
+      const char* p0 = vslot + (2 * kb + j) * 16 * Geo<D>::ROWB + ra.v[db];
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + HALF));
+      const bf16x8 vt = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      R.o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt, p[j], R.o[db], 0, 0, 0);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void store_rows(const Rows<D>& R, const HierFwdArgs& a, int head,
+                                           int lane, float l_tot, float m) {
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (!R.valid) return;
+  uint16_t* op = a.o + (int64_t)R.qtok * a.o_ss + (int64_t)head * a.o_sh;
+  const int half = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = db * 32 + 8 * g4 + 4 * half;
+      u32x2 w;
+      w[0] = (uint32_t)f2bf(R.o[db][4 * g4 + 0] * inv) | ((uint32_t)f2bf(R.o[db][4 * g4 + 1] * inv) << 16);
+      w[1] = (uint32_t)f2bf(R.o[db][4 * g4 + 2] * inv) | ((uint32_t)f2bf(R.o[db][4 * g4 + 3] * inv) << 16);
+      *reinterpret_cast<u32x2*>(op + d0) = w;
+    }
+  if (a.lse && half == 0) {
+    const float lse = l_tot > 0.f ? m * a.scale + __logf(l_tot) : -INFINITY;
+    a.lse[(int64_t)head * a.lse_stride_h + R.qtok] = lse;
+  }
+}
+
+// ---- the kernel ------------------------------------------------------------
+
+template <int D>
+struct Ctx {
+  const char* gk;
+  const char* gv;
+  const int32_t* kv_idx;     // tile_kv_idx + kv_off
+  const uint32_t* kv_mask;   // tile_kv_mask + kv_off
+  const uint32_t* blk;       // tile_blk_and + kv_off / 64
+  uint32_t k_ss_b, v_ss_b;
+  float c2, thr;
+  int nt, wave, lane;
+  bool active;
+  Copier<D> cp;
+  ReadAddr<D> ra;
+};
+
+// Half-step j = 2t + B of the pipeline: QK of block B of tile t+1 into sq,
+// softmax of block j+1 (sc: block 1 of tile t for B = 0, block 0 of tile t+1
+// for B = 1) into pn, PV of block B of tile t with pv; then the masks of sq.
+// The three streams are independent, so one scheduling region interleaves
+// them: each MFMA is followed by a few softmax VALU instructions and the LDS
+// reads of the MFMAs two or three slots ahead.  PAR = t & 1 selects the LDS
+// stages: K(t+1) and its masks in PAR^1, V(t) in PAR.
+template <int D, int PAR, int B>
+__device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& sq,
+                                          const f32x16& sc, const bf16x8* pv, bf16x8* pn,
+                                          bool& resc, float& alpha_pend, char* lds) {
+  constexpr int TB = Geo<D>::TILEB;
+  if (resc) rescale<D>(R, alpha_pend);
+  sq = qk_block<D>(R.q, lds + Geo<D>::KOFF + (PAR ^ 1) * TB, c.ra, B);
+  resc = softmax_block<D>(R, sc, pn, c.c2, c.thr);
+  alpha_pend = R.alpha;
+  // keep the softmax results in this region (otherwise they sink into later
+  // blocks, away from the MFMAs they are meant to overlap)
+  asm volatile("" : "+v"(pn[0]), "+v"(pn[1]), "+v"(R.l), "+v"(alpha_pend));
+  pv_block<D>(R, pv, lds + Geo<D>::VOFF + PAR * TB, c.ra, B);
+  // NC + 2*NDB MFMAs and NC + 4*NDB LDS reads: three reads per two MFMAs
+  constexpr int NM = Geo<D>::NC + 2 * Geo<D>::NDB;
+  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i % 2 == 0)
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    else
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+  }
+  if ((c.blk[t + 1] & R.bits) != R.bits)
+    mask_block(sq, lds + Geo<D>::MOFF + (PAR ^ 1) * Geo<D>::MBYTES, B, R.qframe, c.lane);
+}
+
+// Tile iteration t (t + 1 < nt): copies K(t+2) + masks into stage PAR and
+// V(t+1) into stage PAR^1, runs half-steps 2t and 2t+1.  Invariant on entry:
+// K(t+1), masks(t+1) and V(t) resident; S(2t+1) (sb) masked; P(2t) (pa)
+// ready with its rescale pending.
+template <int D, int PAR>
+__device__ __forceinline__ void tile_iter(Ctx<D>& c, Rows<D>& R, int t, f32x16& sa, f32x16& sb,
+                                          bf16x8* pa, bf16x8* pb, bool& resc, float& alpha_pend,
+                                          Idx<D>& ik, Idx<D>& iv, char* lds) {
+  constexpr int TB = Geo<D>::TILEB;
+  if (t + 2 < c.nt) {
+    copy_tile<D, false>(c.gk, c.k_ss_b, c.cp, ik, lds + Geo<D>::KOFF + PAR * TB, c.wave);
+    if (c.wave == 0)
+      copy_masks(c.kv_mask + (t + 2) * kSlab, lds + Geo<D>::MOFF + PAR * Geo<D>::MBYTES, c.lane);
+  }
+  copy_tile<D, true>(c.gv, c.v_ss_b, c.cp, iv, lds + Geo<D>::VOFF + (PAR ^ 1) * TB, c.wave);
+  ik = load_idx<D>(c.kv_idx, min(t + 3, c.nt - 1), c.cp.idx_off);
+  iv = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.cp.idx_off);
+  if (c.active) {
+    half_step<D, PAR, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, lds);
+    half_step<D, PAR, 1>(c, R, t, sb, sa, pb, pa, resc, alpha_pend, lds);
+  }
+  wait_copies();
+  __syncthreads();
+}
+
+// Last tile (t = nt - 1): softmax of its block 1 (sb) into pb, PV of both
+// blocks, then the output rows.
+template <int D, int PAR>
+__device__ __forceinline__ void tail(Ctx<D>& c, Rows<D>& R, const HierFwdArgs& a, int head,
+                                     const f32x16& sb, const bf16x8* pa, bf16x8* pb, bool resc,
+                                     float alpha_pend, char* lds) {
+  const char* vs = lds + Geo<D>::VOFF + PAR * Geo<D>::TILEB;
+  if (resc) rescale<D>(R, alpha_pend);
+  resc = softmax_block<D>(R, sb, pb, c.c2, c.thr);
+  alpha_pend = R.alpha;
+  pv_block<D>(R, pa, vs, c.ra, 0);
+  if (resc) rescale<D>(R, alpha_pend);
+  pv_block<D>(R, pb, vs, c.ra, 1);
+  store_rows<D>(R, a, head, c.lane, pair_sum(R.l), R.m);
 }
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, int total) {
-  constexpr int NC = D / 16;   // d-chunks of QK^T
-  constexpr int NDB = D / 32;  // d-blocks of O^T
-  constexpr int KPK = Tile<D>::kPitchK;
-  constexpr int KPV = Tile<D>::kPitchV;
-  constexpr int NV = D / 32;   // 16-byte vectors per thread per K (or V) tile
-  __shared__ __align__(16) Smem<D> sm;
-
+  __shared__ __align__(16) char lds[Geo<D>::LDS];
   // XCD-aware mapping: consecutive logical items land on the same XCD (the
-  // dispatcher round-robins workgroups over 8 XCDs), so the items sharing a
-  // head and overlapping key windows share one L2.
+  // dispatcher round-robins workgroups over 8 XCDs), so items sharing a head
+  // and overlapping key windows share one L2.
   const int G = gridDim.x;
   const int bid = blockIdx.x;
   const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
   if (logical >= total) return;
   const int head = logical / a.n_items;
   const int item = logical - head * a.n_items;
-
   const int32_t* it = a.tile_items + (int64_t)item * 8;
-  const int qbase = it[0], qstride = it[1], qlen = it[2];
-  const int row_start = it[3], row_count = it[4];
-  const int kv_off = it[5], kv_cnt = it[6];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int half = lane >> 5, col = lane & 31;
+  Ctx<D> c;
+  c.lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row_count = it[4], kv_off = it[5], kv_cnt = it[6];
+  c.nt = kv_cnt / kSlab;
+  c.active = c.wave * 32 < row_count;
+  c.c2 = a.scale * 1.4426950408889634f;
+  c.thr = kRescaleLog2 / c.c2;
+  c.gk = reinterpret_cast<const char*>(a.k + (int64_t)head * a.k_sh);
+  c.gv = reinterpret_cast<const char*>(a.v + (int64_t)head * a.v_sh);
+  c.k_ss_b = (uint32_t)(a.k_ss * 2);
+  c.v_ss_b = (uint32_t)(a.v_ss * 2);
+  c.kv_idx = a.tile_kv_idx + kv_off;
+  c.kv_mask = a.tile_kv_mask + kv_off;
+  c.blk = a.tile_blk_and + kv_off / kSlab;
+  c.cp.init(c.wave, c.lane);
+  c.ra.init(c.lane);
 
-  // this lane's query row
-  const int rrel = wave * 32 + col;
-  const bool valid = rrel < row_count;
-  const int ri = row_start + (valid ? rrel : 0);
-  const int qframe = ri / qlen;
-  const int qtok = qbase + qframe * qstride + (ri - qframe * qlen);
-  const bool wave_active = wave * 32 < row_count;
-  const uint32_t wave_bits = wave_or(valid ? (1u << qframe) : 0u);
+  Rows<D> R;
+  rows_init<D>(R, a, it, head, c.wave * 32, c.lane);
+  const int nt = c.nt;
+  if (nt == 0) {
+    if (c.active) store_rows<D>(R, a, head, c.lane, 0.f, -INFINITY);
+    return;
+  }
+  constexpr int TB = Geo<D>::TILEB;
+  char* const kst0 = lds + Geo<D>::KOFF;
+  char* const vst0 = lds + Geo<D>::VOFF;
+  char* const mst0 = lds + Geo<D>::MOFF;
 
-  // Q fragments (B operand of S^T = K Q^T): row qtok, d = 16c + 8*half + [0,8)
-  bf16x8 qf[NC];
+  // prologue: K(0), V(0), K(1) and masks(0, 1) resident; S(0), S(1) (both
+  // blocks of tile 0) computed and masked; P(0) from the softmax of S(0).
   {
-    const uint16_t* qp = a.q + (int64_t)qtok * a.q_ss + (int64_t)head * a.q_sh + 8 * half;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(qp + 16 * c);
-  }
-
-  // loaders (every thread moves NV 16-byte vectors of K and of V per tile):
-  //  K: key = tid % 64, elements [q*D/4, (q+1)*D/4) with q = tid / 64
-  //  V: 16-lane group m = tid / 16 stores keys 8*(m%8) + i/2 (i = tid % 16),
-  //     16-byte chunk 2*((m/8)*NV + e) + i%2 for vector e
-  const int kkey = tid & 63, kq = tid >> 6;
-  const int vgrp = tid >> 4, vi = tid & 15;
-  const int vkey = 8 * (vgrp & 7) + (vi >> 1);
-  const int64_t k_head = (int64_t)head * a.k_sh, v_head = (int64_t)head * a.v_sh;
-  u32x4 kreg[NV], vreg[NV];
-  uint32_t mreg = 0;
-  const int ntiles = kv_cnt / kKT;
-  int kidx = 0, vidx = 0;   // K/V pool rows of the next tile to fetch
-
-  auto fetch_idx = [&](int t) {   // t < ntiles
-    const int base = kv_off + t * kKT;
-    kidx = a.tile_kv_idx[base + kkey];
-    vidx = a.tile_kv_idx[base + vkey];
-  };
-  auto gload = [&](int t) {       // uses kidx / vidx fetched for tile t
-    const uint16_t* kp = a.k + (int64_t)kidx * a.k_ss + k_head + kq * (D / 4);
-    const uint16_t* vp = a.v + (int64_t)vidx * a.v_ss + v_head;
-#pragma unroll
-    for (int e = 0; e < NV; ++e) {
-      kreg[e] = *reinterpret_cast<const u32x4*>(kp + 8 * e);
-      const int chunk = 2 * ((vgrp >> 3) * NV + e) + (vi & 1);
-      vreg[e] = *reinterpret_cast<const u32x4*>(vp + 8 * chunk);
+    const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.cp.idx_off);
+    copy_tile<D, false>(c.gk, c.k_ss_b, c.cp, i0, kst0, c.wave);
+    copy_tile<D, true>(c.gv, c.v_ss_b, c.cp, i0, vst0, c.wave);
+    if (c.wave == 0) copy_masks(c.kv_mask, mst0, c.lane);
+    if (nt > 1) {
+      const Idx<D> i1 = load_idx<D>(c.kv_idx, 1, c.cp.idx_off);
+      copy_tile<D, false>(c.gk, c.k_ss_b, c.cp, i1, kst0 + TB, c.wave);
+      if (c.wave == 0) copy_masks(c.kv_mask + kSlab, mst0 + Geo<D>::MBYTES, c.lane);
     }
-    if (tid < kKT) mreg = a.tile_kv_mask[kv_off + t * kKT + tid];
-  };
-  auto lstore = [&](int buf) {
-    uint16_t* kd = &sm.k[buf][kkey * KPK + kq * (D / 4)];
-    uint16_t* vd = &sm.v[buf][vkey * KPV];
-#pragma unroll
-    for (int e = 0; e < NV; ++e) {
-      *reinterpret_cast<u32x4*>(kd + 8 * e) = kreg[e];
-      const int chunk = 2 * ((vgrp >> 3) * NV + e) + (vi & 1);
-      *reinterpret_cast<u32x4*>(vd + 8 * chunk) = vreg[e];
-    }
-    if (tid < kKT) sm.km[buf][tid] = mreg;
-  };
-
-  const float c2 = a.scale * 1.4426950408889634f;  // softmax scale * log2(e)
-  const float thr = kRescaleLog2 / c2;             // lazy-rescale margin in score units
-  float m_ref = -INFINITY, l_run = 0.f;
-  f32x16 o[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
-  const f32x16 zero = {};
-
-  if (ntiles > 0) {
-    fetch_idx(0);
-    gload(0);
-    lstore(0);
-    fetch_idx(ntiles > 1 ? 1 : 0);
-  }
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    // Prefetch tile t+1 unconditionally (the last iteration re-reads tile t):
-    // a conditional load here makes the compiler wait on it before the MFMAs.
-    const int tn = t + 1 < ntiles ? t + 1 : t;
-    gload(tn);
-    fetch_idx(t + 2 < ntiles ? t + 2 : tn);
-    if (wave_active) {
-      // ---- S^T = K Q^T -------------------------------------------------------
-      f32x16 s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const uint16_t* kp = &sm.k[buf][(kb * 32 + col) * KPK + 8 * half];
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            *reinterpret_cast<const bf16x8*>(kp), qf[0], zero, 0, 0, 0);
-#pragma unroll
-        for (int c = 1; c < NC; ++c) {
-          bf16x8 kf = *reinterpret_cast<const bf16x8*>(kp + 16 * c);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], s[kb], 0, 0, 0);
-        }
-      }
-      // ---- visibility ---------------------------------------------------------
-      const uint32_t blk = a.tile_blk_and[kv_off / kKT + t];
-      if ((blk & wave_bits) != wave_bits) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const u32x4 mk = *reinterpret_cast<const u32x4*>(&sm.km[buf][kb * 32 + 8 * g4 + 4 * half]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (!((mk[e] >> qframe) & 1u)) s[kb][4 * g4 + e] = -INFINITY;
-          }
-      }
-      // ---- online softmax (lazy rescale) ----------------------------------------
-      float mx = fmaxf(s[0][0], s[0][1]);
-#pragma unroll
-      for (int r = 2; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[0][r], s[0][r + 1]));
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[1][r], s[1][r + 1]));
-      mx = pair_max(mx);
-      if (__ballot(mx > m_ref + thr) != 0) {
-        const float m_new = fmaxf(m_ref, mx);
-        const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_ref - m_new) * c2);
-        m_ref = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      }
-      const float nb = (m_ref == -INFINITY) ? 0.f : -m_ref * c2;
-      float ps0 = 0.f, ps1 = 0.f;
-      bf16x8 pk[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], c2, nb));
-          if (r & 1) ps1 += p; else ps0 += p;
-          pk[kb * 2 + (r >> 3)][r & 7] = (__bf16)p;
-        }
-      l_run += ps0 + ps1;
-      // ---- O^T += V^T P^T ------------------------------------------------------
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int d0 = db * 32 + 16 * ((lane >> 4) & 1);
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-          const bf16x8 vf = load_vt<KPV>(sm.v[buf], kc, d0, lane);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pk[kc], o[db], 0, 0, 0);
-        }
-      }
-    }
-    if (t + 1 < ntiles) lstore(buf ^ 1);
+    wait_copies();
     __syncthreads();
   }
-
-  if (!wave_active) return;
-  const float l_tot = pair_sum(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (valid) {
-    uint16_t* op = a.o + (int64_t)qtok * a.o_ss + (int64_t)head * a.o_sh;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d0 = db * 32 + 8 * g4 + 4 * half;
-        u32x2 w;
-        w[0] = (uint32_t)f2bf(o[db][4 * g4 + 0] * inv) | ((uint32_t)f2bf(o[db][4 * g4 + 1] * inv) << 16);
-        w[1] = (uint32_t)f2bf(o[db][4 * g4 + 2] * inv) | ((uint32_t)f2bf(o[db][4 * g4 + 3] * inv) << 16);
-        *reinterpret_cast<u32x2*>(op + d0) = w;
-      }
-    if (a.lse && half == 0) {
-      const float lse = l_tot > 0.f ? m_ref * a.scale + __logf(l_tot) : -INFINITY;
-      a.lse[(int64_t)head * a.lse_stride_h + qtok] = lse;
+  Idx<D> ik = load_idx<D>(c.kv_idx, min(2, nt - 1), c.cp.idx_off);
+  Idx<D> iv = load_idx<D>(c.kv_idx, min(1, nt - 1), c.cp.idx_off);
+  f32x16 sa, sb;
+  bf16x8 pa[2], pb[2];
+  bool resc = false;
+  float alpha_pend = 1.f;
+  if (c.active) {
+    sa = qk_block<D>(R.q, kst0, c.ra, 0);
+    sb = qk_block<D>(R.q, kst0, c.ra, 1);
+    if ((c.blk[0] & R.bits) != R.bits) {
+      mask_block(sa, mst0, 0, R.qframe, c.lane);
+      mask_block(sb, mst0, 1, R.qframe, c.lane);
     }
+    resc = softmax_block<D>(R, sa, pa, c.c2, c.thr);
+    alpha_pend = R.alpha;
+  }
+  __syncthreads();   // every wave has read K stage 0 and masks stage 0
+
+  // steady state, two tile iterations per trip so that every LDS stage offset
+  // is a compile-time constant
+  int t = 0;
+  for (; t + 2 < nt; t += 2) {
+    tile_iter<D, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, ik, iv, lds);
+    tile_iter<D, 1>(c, R, t + 1, sa, sb, pa, pb, resc, alpha_pend, ik, iv, lds);
+  }
+  if (t + 1 < nt) {
+    tile_iter<D, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, ik, iv, lds);
+    if (c.active) tail<D, 1>(c, R, a, head, sb, pa, pb, resc, alpha_pend, lds);
+  } else {
+    if (c.active) tail<D, 0>(c, R, a, head, sb, pa, pb, resc, alpha_pend, lds);
   }
 }
 
@@ -306,16 +533,26 @@ extern "C" int hier_attn_fwd(const HierFwdArgs* args, void* stream) {
   HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
   const HierFwdArgs& a = *args;
   HIER_REQUIRE(a.D == 128 || a.D == 64, HIER_EUNSUPPORTED, "head_dim must be 64 or 128, got %d", a.D);
-  HIER_REQUIRE(a.H >= 1 && a.n_items >= 0, HIER_EINVAL, "invalid H=%d n_items=%d", a.H, a.n_items);
+  HIER_REQUIRE(a.H >= 1 && a.n_items >= 0 && a.kv_rows >= 0, HIER_EINVAL,
+               "invalid H=%d n_items=%d kv_rows=%d", a.H, a.n_items, a.kv_rows);
   HIER_REQUIRE(a.q && a.k && a.v && a.o && a.tile_items && a.tile_kv_idx && a.tile_kv_mask &&
                    a.tile_blk_and,
                HIER_EINVAL, "NULL tensor pointer");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
-  HIER_REQUIRE(al16(a.q) && al16(a.k) && al16(a.v) && al16(a.o), HIER_EINVAL,
-               "q/k/v/o must be 16-byte aligned");
+  HIER_REQUIRE(al16(a.q) && al16(a.k) && al16(a.v) && al16(a.o) && al16(a.tile_kv_idx),
+               HIER_EINVAL, "q/k/v/o and the key index list must be 16-byte aligned");
   HIER_REQUIRE(a.q_ss % 8 == 0 && a.q_sh % 8 == 0 && a.k_ss % 8 == 0 && a.k_sh % 8 == 0 &&
                    a.v_ss % 8 == 0 && a.v_sh % 8 == 0 && a.o_ss % 4 == 0 && a.o_sh % 4 == 0,
                HIER_EINVAL, "strides must keep 16-byte rows aligned");
+  HIER_REQUIRE(a.k_ss >= 0 && a.k_sh >= 0 && a.v_ss >= 0 && a.v_sh >= 0, HIER_EINVAL,
+               "K/V strides must be non-negative");
+  // K / V rows are addressed with 32-bit byte offsets from k / v.
+  const int64_t rows = a.kv_rows > 0 ? a.kv_rows - 1 : 0;
+  const int64_t k_ext = (rows * a.k_ss + (int64_t)(a.H - 1) * a.k_sh + a.D) * 2;
+  const int64_t v_ext = (rows * a.v_ss + (int64_t)(a.H - 1) * a.v_sh + a.D) * 2;
+  HIER_REQUIRE(k_ext <= (1ll << 32) && v_ext <= (1ll << 32), HIER_EUNSUPPORTED,
+               "K/V views must span at most 4 GiB (got %lld / %lld bytes)", (long long)k_ext,
+               (long long)v_ext);
   if (a.n_items == 0) return HIER_OK;
   const int64_t total = (int64_t)a.n_items * a.H;
   HIER_REQUIRE(total < (1ll << 31) - 8, HIER_EUNSUPPORTED, "too many work items");

@@ -61,7 +61,7 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
     if k3.shape[1:] != (H, D) or v3.shape[1:] != (H, D) or o3.shape[1:] != (H, D):
         raise ValueError("q/k/v/out head shapes differ")
     if tiles.rows_per_item != 128:
-        raise ValueError("hier_attn_fwd processes work items of exactly 128 query rows")
+        raise ValueError("hier_attn_fwd processes work items of up to 128 query rows")
     if k3.shape[0] < tiles.key_extent or v3.shape[0] < tiles.key_extent:
         raise ValueError(f"K/V hold {k3.shape[0]} rows, the tile list addresses {tiles.key_extent}")
     if q3.shape[0] < tiles.row_extent or o3.shape[0] < tiles.row_extent:
@@ -74,6 +74,7 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
         return out
     args = _capi.HierFwdArgs(
         H=H, D=D, n_items=last - first, scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
+        kv_rows=min(k3.shape[0], v3.shape[0]), reserved=0,
         q=q3.data_ptr(), k=k3.data_ptr(), v=v3.data_ptr(), o=o3.data_ptr(),
         lse=None if lse is None else lse.data_ptr(),
         q_ss=q_ss, q_sh=q_sh, k_ss=k_ss, k_sh=k_sh, v_ss=v_ss, v_sh=v_sh, o_ss=o_ss, o_sh=o_sh,

@@ -35,7 +35,7 @@ import torch
 from . import _capi
 
 TILE_KEYS = 64          # attention kernel key tile
-ROWS_PER_ITEM = 128     # attention kernel query rows per work item
+ROWS_PER_ITEM = 128     # attention kernel query rows per work item (4 waves x 32)
 SEG_ROUND = 64          # hier_segmented_attention.py:371
 TILED_N = 128           # hier_tiled_attention.py:33
 TILED_M = 16            # hier_tiled_attention.py:32

@@ -70,7 +70,9 @@ def test_forward_matches_oracle_labels(case):
     dead = torch.from_numpy(inactive_local_rows(topo))
     got = lse.cpu()
     assert torch.isneginf(got[:, dead]).all()
-    assert (got[:, ~dead] - ref_lse[:, ~dead]).abs().max() < 1e-3
+    # the kernel's row sum adds the bf16-rounded weights that multiply V, so
+    # its normaliser differs from an fp32 sum by at most 2^-9 relative
+    assert (got[:, ~dead] - ref_lse[:, ~dead]).abs().max() < 2.0 ** -8
 
 
 def test_forward_dynamic_membership_matches_oracle():
