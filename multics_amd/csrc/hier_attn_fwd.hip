@@ -34,145 +34,27 @@
 // masks) and V tile t+1 are in flight; two K, two V and two mask stages fill
 // 65 KB of LDS per workgroup.
 //
-// LDS layout of a tile: key rows of 2*D bytes with no padding.  Key j of a
-// 16-key group sits in row NR*(j % NI) + j / NI of the group (NI = D/32 copy
-// instructions per wave, NR = 64 lanes / (D/8) chunks = rows per instruction),
-// so each lane copies NI consecutive keys of one row slot.  16-byte chunks are
-// XOR-swizzled per key (K: every 16 consecutive keys of one chunk column land
-// in 16 different bank groups; V: the 4 rows x 4 chunks of one transposed read
-// land in 16 different bank groups).
+// The LDS tile layout and the copies are described in hier_tile.h.
 #include "hier_common.h"
+#include "hier_tile.h"
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef const __attribute__((address_space(1))) void gbl_void;
+using namespace hier::tile;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kSlab = 64;              // keys per LDS tile
 constexpr float kRescaleLog2 = 8.0f;   // lazy-rescale threshold (exp2 units)
 
+// LDS of a workgroup: K[2] | V[2] | masks[2] (one dword per key).  K tiles are
+// only read as rows, V tiles only transposed.
 template <int D>
-struct Geo {
-  static constexpr int ROWB = 2 * D;                // bytes per key row
-  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int NI = D / 32;                 // copy instructions per wave per tile
-  static constexpr int NR = 64 / CPR;               // rows per copy instruction
-  static constexpr int TILEB = kSlab * ROWB;
-  static constexpr int MBYTES = kSlab * 4;
+struct Lds {
   static constexpr int KOFF = 0;
-  static constexpr int VOFF = 2 * TILEB;
-  static constexpr int MOFF = 4 * TILEB;
-  static constexpr int LDS = 4 * TILEB + 2 * MBYTES;
-  static constexpr int NC = D / 16;                 // d-chunks of QK^T
-  static constexpr int NDB = D / 32;                // d-blocks of O^T
-  static_assert(NI * NR == 16, "a wave copies 16 keys per tile");
+  static constexpr int VOFF = 2 * Geo<D>::TILEB;
+  static constexpr int MOFF = 4 * Geo<D>::TILEB;
+  static constexpr int SIZE = 4 * Geo<D>::TILEB + 2 * Geo<D>::MBYTES;
 };
-
-// Row of key `key` inside its tile.
-template <int D>
-__device__ __forceinline__ int prow(int key) {
-  const int j = key & 15;
-  return (key & ~15) + Geo<D>::NR * (j % Geo<D>::NI) + j / Geo<D>::NI;
-}
-// Chunk swizzles (XOR masks on the 16-byte chunk index of a row).
-template <int D>
-__device__ __forceinline__ int swz_k(int key) {
-  return D == 128 ? (key & 15) : ((key & 1) | ((key >> 1) & 6));
-}
-template <int D>
-__device__ __forceinline__ int swz_v(int key) {
-  return D == 128 ? 4 * (key & 3) : 4 * (key & 1);
-}
-
-__device__ __forceinline__ float pair_max(float v) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float pair_sum(float v) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ uint32_t wave_or(uint32_t v) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) v |= __shfl_xor(v, d, 64);
-  return v;
-}
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  return __builtin_bit_cast(uint16_t, (__bf16)f);  // round to nearest even
-}
-
-// ---- tile copies (global -> LDS) -------------------------------------------
-
-// Per-lane constants of the tile copies: the lane copies chunk pc of row slot
-// r for keys 16*wave + NI*r + e, e < NI.  With that key order the swizzled
-// chunk of copy e is (pk ^ e) for K and (pc ^ 4e) for V.
-template <int D>
-struct Copier {
-  uint32_t pk16, pc16;   // 16 * pk, 16 * pc
-  int idx_off;           // first key of the lane inside a tile
-  __device__ __forceinline__ void init(int wave, int lane) {
-    const int r = lane / Geo<D>::CPR, pc = lane % Geo<D>::CPR;
-    idx_off = 16 * wave + Geo<D>::NI * r;
-    const int pk = pc ^ (swz_k<D>(idx_off) & ~(Geo<D>::NI - 1));
-    pk16 = 16u * (uint32_t)pk;
-    pc16 = 16u * (uint32_t)pc;
-  }
-  __device__ __forceinline__ uint32_t add_k(int e) const { return pk16 ^ (16u * e); }
-  __device__ __forceinline__ uint32_t add_v(int e) const { return pc16 ^ (64u * e); }
-};
-
-template <int D>
-struct Idx {
-  int v[Geo<D>::NI];
-};
-
-template <int D>
-__device__ __forceinline__ Idx<D> load_idx(const int32_t* kv_idx, int tile, int idx_off) {
-  Idx<D> r;
-  const int32_t* p = kv_idx + tile * kSlab + idx_off;
-  if constexpr (Geo<D>::NI == 4) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r.v[e] = (int)w[e];
-  } else {
-    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
-#pragma unroll
-    for (int e = 0; e < 2; ++e) r.v[e] = (int)w[e];
-  }
-  return r;
-}
-
-// One operand tile: NI 16-byte copies per lane, 1 KB per wave instruction.
-// g points at head `head` of row 0 of K (IS_V false) or V.
-template <int D, bool IS_V>
-__device__ __forceinline__ void copy_tile(const char* g, uint32_t ss_bytes, const Copier<D>& cp,
-                                          const Idx<D>& ix, char* slot, int wave) {
-#pragma unroll
-  for (int e = 0; e < Geo<D>::NI; ++e) {
-    const uint32_t off = (uint32_t)ix.v[e] * ss_bytes + (IS_V ? cp.add_v(e) : cp.add_k(e));
-    __builtin_amdgcn_global_load_lds(
-        (gbl_void*)(g + off),
-        (lds_void*)(slot + (16 * wave + Geo<D>::NR * e) * Geo<D>::ROWB), 16, 0, 0);
-  }
-}
-
-// Visibility masks of one tile (one dword per key, natural key order).
-__device__ __forceinline__ void copy_masks(const uint32_t* m, char* slot, int lane) {
-  __builtin_amdgcn_global_load_lds((gbl_void*)(m + lane), (lds_void*)slot, 4, 0, 0);
-}
-
-__device__ __forceinline__ void wait_copies() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), other counters untouched
-}
 
 // ---- per-sub-block state and math ------------------------------------------
 
@@ -211,19 +93,13 @@ __device__ __forceinline__ void rows_init(Rows<D>& R, const HierFwdArgs& a, cons
 // Per-lane LDS byte offsets of the MFMA operand reads (tile-relative).
 template <int D>
 struct ReadAddr {
-  int k[Geo<D>::NC];     // K row of key (lane & 31), chunk (lane >> 5) + 2c
+  int k[Geo<D>::NC];     // K rows: key (lane & 31), chunk (lane >> 5) + 2c
   int v[Geo<D>::NDB];    // first transposed V read of d-block db, key chunk 0
   __device__ __forceinline__ void init(int lane) {
-    const int kk = lane & 31;
 #pragma unroll
-    for (int c = 0; c < Geo<D>::NC; ++c)
-      k[c] = prow<D>(kk) * Geo<D>::ROWB + 16 * (((lane >> 5) + 2 * c) ^ swz_k<D>(kk));
-    const int i = lane & 15;
-    const int key = 4 * (lane >> 5) + (i >> 2);
-    const int q = 2 * ((lane >> 4) & 1) + ((i & 3) >> 1);
+    for (int c = 0; c < Geo<D>::NC; ++c) k[c] = row_read_off<D, kRowRead>(lane, c);
 #pragma unroll
-    for (int db = 0; db < Geo<D>::NDB; ++db)
-      v[db] = prow<D>(key) * Geo<D>::ROWB + 16 * ((4 * db + q) ^ swz_v<D>(key)) + 8 * (i & 1);
+    for (int db = 0; db < Geo<D>::NDB; ++db) v[db] = tr_read_off<D, kTrRead>(lane, db, 0);
   }
 };
 
@@ -309,9 +185,7 @@ __device__ __forceinline__ void pv_block(Rows<D>& R, const bf16x8* p, const char
 #pragma unroll
     for (int db = 0; db < Geo<D>::NDB; ++db) {
       const char* p0 = vslot + (2 * kb + j) * 16 * Geo<D>::ROWB + ra.v[db];
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + HALF));
-      const bf16x8 vt = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      const bf16x8 vt = tr_read(p0, p0 + HALF);   // kTrRead: keys +8 are HALF further
       R.o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt, p[j], R.o[db], 0, 0, 0);
     }
 }
@@ -352,7 +226,8 @@ struct Ctx {
   float c2, thr;
   int nt, wave, lane;
   bool active;
-  Copier<D> cp;
+  Copier<D, kRowRead> ck;
+  Copier<D, kTrRead> cv;
   ReadAddr<D> ra;
 };
 
@@ -369,13 +244,13 @@ __device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
                                           bool& resc, float& alpha_pend, char* lds) {
   constexpr int TB = Geo<D>::TILEB;
   if (resc) rescale<D>(R, alpha_pend);
-  sq = qk_block<D>(R.q, lds + Geo<D>::KOFF + (PAR ^ 1) * TB, c.ra, B);
+  sq = qk_block<D>(R.q, lds + Lds<D>::KOFF + (PAR ^ 1) * TB, c.ra, B);
   resc = softmax_block<D>(R, sc, pn, c.c2, c.thr);
   alpha_pend = R.alpha;
   // keep the softmax results in this region (otherwise they sink into later
   // blocks, away from the MFMAs they are meant to overlap)
   asm volatile("" : "+v"(pn[0]), "+v"(pn[1]), "+v"(R.l), "+v"(alpha_pend));
-  pv_block<D>(R, pv, lds + Geo<D>::VOFF + PAR * TB, c.ra, B);
+  pv_block<D>(R, pv, lds + Lds<D>::VOFF + PAR * TB, c.ra, B);
   // NC + 2*NDB MFMAs and NC + 4*NDB LDS reads: three reads per two MFMAs
   constexpr int NM = Geo<D>::NC + 2 * Geo<D>::NDB;
   __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
@@ -389,7 +264,7 @@ __device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
     __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
   }
   if ((c.blk[t + 1] & R.bits) != R.bits)
-    mask_block(sq, lds + Geo<D>::MOFF + (PAR ^ 1) * Geo<D>::MBYTES, B, R.qframe, c.lane);
+    mask_block(sq, lds + Lds<D>::MOFF + (PAR ^ 1) * Geo<D>::MBYTES, B, R.qframe, c.lane);
 }
 
 // Tile iteration t (t + 1 < nt): copies K(t+2) + masks into stage PAR and
@@ -402,13 +277,13 @@ __device__ __forceinline__ void tile_iter(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
                                           Idx<D>& ik, Idx<D>& iv, char* lds) {
   constexpr int TB = Geo<D>::TILEB;
   if (t + 2 < c.nt) {
-    copy_tile<D, false>(c.gk, c.k_ss_b, c.cp, ik, lds + Geo<D>::KOFF + PAR * TB, c.wave);
+    copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, ik, lds + Lds<D>::KOFF + PAR * TB, c.wave);
     if (c.wave == 0)
-      copy_masks(c.kv_mask + (t + 2) * kSlab, lds + Geo<D>::MOFF + PAR * Geo<D>::MBYTES, c.lane);
+      copy_dwords(c.kv_mask + (t + 2) * kSlab, lds + Lds<D>::MOFF + PAR * Geo<D>::MBYTES, c.lane);
   }
-  copy_tile<D, true>(c.gv, c.v_ss_b, c.cp, iv, lds + Geo<D>::VOFF + (PAR ^ 1) * TB, c.wave);
-  ik = load_idx<D>(c.kv_idx, min(t + 3, c.nt - 1), c.cp.idx_off);
-  iv = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.cp.idx_off);
+  copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, iv, lds + Lds<D>::VOFF + (PAR ^ 1) * TB, c.wave);
+  ik = load_idx<D>(c.kv_idx, min(t + 3, c.nt - 1), c.ck.idx_off);
+  iv = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
   if (c.active) {
     half_step<D, PAR, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, lds);
     half_step<D, PAR, 1>(c, R, t, sb, sa, pb, pa, resc, alpha_pend, lds);
@@ -423,7 +298,7 @@ template <int D, int PAR>
 __device__ __forceinline__ void tail(Ctx<D>& c, Rows<D>& R, const HierFwdArgs& a, int head,
                                      const f32x16& sb, const bf16x8* pa, bf16x8* pb, bool resc,
                                      float alpha_pend, char* lds) {
-  const char* vs = lds + Geo<D>::VOFF + PAR * Geo<D>::TILEB;
+  const char* vs = lds + Lds<D>::VOFF + PAR * Geo<D>::TILEB;
   if (resc) rescale<D>(R, alpha_pend);
   resc = softmax_block<D>(R, sb, pb, c.c2, c.thr);
   alpha_pend = R.alpha;
@@ -435,7 +310,7 @@ __device__ __forceinline__ void tail(Ctx<D>& c, Rows<D>& R, const HierFwdArgs& a
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, int total) {
-  __shared__ __align__(16) char lds[Geo<D>::LDS];
+  __shared__ __align__(16) char lds[Lds<D>::SIZE];
   // XCD-aware mapping: consecutive logical items land on the same XCD (the
   // dispatcher round-robins workgroups over 8 XCDs), so items sharing a head
   // and overlapping key windows share one L2.
@@ -463,7 +338,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
   c.kv_idx = a.tile_kv_idx + kv_off;
   c.kv_mask = a.tile_kv_mask + kv_off;
   c.blk = a.tile_blk_and + kv_off / kSlab;
-  c.cp.init(c.wave, c.lane);
+  c.ck.init(c.wave, c.lane);
+  c.cv.init(c.wave, c.lane);
   c.ra.init(c.lane);
 
   Rows<D> R;
@@ -474,27 +350,27 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
     return;
   }
   constexpr int TB = Geo<D>::TILEB;
-  char* const kst0 = lds + Geo<D>::KOFF;
-  char* const vst0 = lds + Geo<D>::VOFF;
-  char* const mst0 = lds + Geo<D>::MOFF;
+  char* const kst0 = lds + Lds<D>::KOFF;
+  char* const vst0 = lds + Lds<D>::VOFF;
+  char* const mst0 = lds + Lds<D>::MOFF;
 
   // prologue: K(0), V(0), K(1) and masks(0, 1) resident; S(0), S(1) (both
   // blocks of tile 0) computed and masked; P(0) from the softmax of S(0).
   {
-    const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.cp.idx_off);
-    copy_tile<D, false>(c.gk, c.k_ss_b, c.cp, i0, kst0, c.wave);
-    copy_tile<D, true>(c.gv, c.v_ss_b, c.cp, i0, vst0, c.wave);
-    if (c.wave == 0) copy_masks(c.kv_mask, mst0, c.lane);
+    const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
+    copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i0, kst0, c.wave);
+    copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, i0, vst0, c.wave);
+    if (c.wave == 0) copy_dwords(c.kv_mask, mst0, c.lane);
     if (nt > 1) {
-      const Idx<D> i1 = load_idx<D>(c.kv_idx, 1, c.cp.idx_off);
-      copy_tile<D, false>(c.gk, c.k_ss_b, c.cp, i1, kst0 + TB, c.wave);
-      if (c.wave == 0) copy_masks(c.kv_mask + kSlab, mst0 + Geo<D>::MBYTES, c.lane);
+      const Idx<D> i1 = load_idx<D>(c.kv_idx, 1, c.ck.idx_off);
+      copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i1, kst0 + TB, c.wave);
+      if (c.wave == 0) copy_dwords(c.kv_mask + kSlab, mst0 + Geo<D>::MBYTES, c.lane);
     }
     wait_copies();
     __syncthreads();
   }
-  Idx<D> ik = load_idx<D>(c.kv_idx, min(2, nt - 1), c.cp.idx_off);
-  Idx<D> iv = load_idx<D>(c.kv_idx, min(1, nt - 1), c.cp.idx_off);
+  Idx<D> ik = load_idx<D>(c.kv_idx, min(2, nt - 1), c.ck.idx_off);
+  Idx<D> iv = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
   f32x16 sa, sb;
   bf16x8 pa[2], pb[2];
   bool resc = false;
