@@ -187,6 +187,51 @@ typedef struct HierFwdArgs {
 
 int hier_attn_fwd(const HierFwdArgs* args, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Backward of hier_attn_fwd: dQ, dK, dV.  Replaces the autograd backward of */
+/* the Flex path the training forward differentiates through               */
+/* (attention.py:322-353, 367-434; hier_masks.py:690-719).                  */
+/* Two launches on `stream`: a query-major pass over the forward tile list   */
+/* (dQ; also writes delta = rowsum(dO * O) and lse2 = lse * log2(e) into the */
+/* caller's workspace) and a key-major pass over the transposed tile list     */
+/* (dK, dV), so every gradient row is written by exactly one workgroup: no   */
+/* atomics, deterministic.  Gradient rows that no item covers are untouched; */
+/* key rows of a key item that no query sees are written as 0.             */
+/* ------------------------------------------------------------------------ */
+typedef struct HierBwdArgs {
+  int32_t H, D;                    /* heads, head dim (64 or 128)              */
+  int32_t n_items;                 /* query-major items (forward tile list)    */
+  int32_t n_key_items;             /* key-major items (transposed tile list)   */
+  float scale;                     /* softmax scale of the forward             */
+  int32_t kv_rows;                 /* rows addressable in k / v                */
+  int32_t q_rows;                  /* rows addressable in q / dout             */
+  int32_t reserved;                /* must be 0                                */
+  const uint16_t* q;               /* bf16 inputs of the forward               */
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;               /* bf16 forward output                      */
+  const uint16_t* dout;            /* bf16 gradient of the output              */
+  const float* lse;                /* [H][.] natural-log LSE from the forward  */
+  float* delta;                    /* [H][.] workspace, written                */
+  float* lse2;                     /* [H][.] workspace, written                */
+  uint16_t* dq;                    /* bf16 gradients                           */
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t q_ss, q_sh, k_ss, k_sh, v_ss, v_sh, o_ss, o_sh, do_ss, do_sh;
+  int64_t dq_ss, dq_sh, dk_ss, dk_sh, dv_ss, dv_sh;
+  int64_t lse_stride_h;            /* elements between heads of lse / delta / lse2 */
+  const int32_t* tile_items;       /* forward (query-major) tile list          */
+  const int32_t* tile_kv_idx;
+  const uint32_t* tile_kv_mask;
+  const uint32_t* tile_blk_and;
+  const int32_t* key_items;        /* transposed (key-major) tile list: items  */
+  const int32_t* key_q_idx;        /* describe key rows, lists hold query rows */
+  const uint32_t* key_q_mask;      /* bit f: the query sees key frame f        */
+  const uint32_t* key_blk_and;
+} HierBwdArgs;
+
+int hier_attn_bwd(const HierBwdArgs* args, void* stream);
+
 /* Last error message of the calling thread ("" if none).                    */
 const char* hier_last_error(void);
 

@@ -73,11 +73,24 @@ class HierFwdArgs(C.Structure):
                [(n, vp) for n in ("tile_items", "tile_kv_idx", "tile_kv_mask", "tile_blk_and")]
 
 
+class HierBwdArgs(C.Structure):
+    _fields_ = [("H", i32), ("D", i32), ("n_items", i32), ("n_key_items", i32), ("scale", f32),
+                ("kv_rows", i32), ("q_rows", i32), ("reserved", i32)] + \
+               [(n, vp) for n in ("q", "k", "v", "o", "dout", "lse", "delta", "lse2", "dq", "dk",
+                                  "dv")] + \
+               [(n, i64) for n in ("q_ss", "q_sh", "k_ss", "k_sh", "v_ss", "v_sh", "o_ss", "o_sh",
+                                   "do_ss", "do_sh", "dq_ss", "dq_sh", "dk_ss", "dk_sh", "dv_ss",
+                                   "dv_sh", "lse_stride_h")] + \
+               [(n, vp) for n in ("tile_items", "tile_kv_idx", "tile_kv_mask", "tile_blk_and",
+                                  "key_items", "key_q_idx", "key_q_mask", "key_blk_and")]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
+    "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],
     "hier_last_error": [],
     "hier_version": [],
 }

@@ -1,0 +1,481 @@
+// Backward of the block-sparse frame-causal attention for gfx950 (CDNA4).
+//
+// With P = exp(scale * Q K^T - lse) (lse from the forward), dP = dO V^T,
+// delta = rowsum(dO * O) and dS = P * (dP - delta):
+//   dQ = scale * dS K,   dK = scale * dS^T Q,   dV = P^T dO.
+// Two kernels, each writing every gradient row from exactly one workgroup
+// (deterministic, no atomics):
+//
+// dq_kernel   query-major, over the forward tile list (128 query rows per
+//             item, 4 waves x 32).  Per 32-key block:
+//               S^T  = K Q^T          (K rows from LDS, Q^T in registers)
+//               dP^T = V dO^T         (V rows from LDS, dO^T in registers)
+//               dS^T = P^T (dP^T - delta)
+//               dQ^T += K^T dS^T      (K transposed out of LDS)
+//             Also writes delta and lse2 = lse * log2(e) per query row.
+// dkdv_kernel key-major, over the transposed tile list (128 key rows per
+//             item, lists of query rows with a bitmask over key frames).  Per
+//             32-query block:
+//               S  = Q K^T,  dP = dO V^T   (Q / dO rows from LDS, K^T / V^T
+//                                           in registers)
+//               dV^T += dO^T P,  dK^T += Q^T dS   (Q / dO transposed out of LDS)
+// The lane layouts are the forward's: an MFMA result keeps one column per
+// lane and its rows {8*(r/4) + 4*(lane/32) + r%4}, which is exactly the
+// permuted k order of the next MFMA's register operand, so P and dS go from
+// the accumulators to bf16 operands without any shuffle.  Tiles are copied
+// with global_load_lds_dwordx4 into the swizzled layouts of hier_tile.h.
+#include "hier_common.h"
+#include "hier_tile.h"
+
+namespace {
+
+using namespace hier::tile;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---- shared helpers --------------------------------------------------------
+
+template <int D>
+__device__ __forceinline__ void load_row(bf16x8* dst, const uint16_t* row, int lane) {
+  const uint16_t* p = row + 8 * (lane >> 5);
+#pragma unroll
+  for (int c = 0; c < Geo<D>::NC; ++c) dst[c] = *reinterpret_cast<const bf16x8*>(p + 16 * c);
+}
+
+template <int D>
+__device__ __forceinline__ f32x16 row_mfma(const bf16x8* b, const char* tile, const int* off,
+                                           int blk) {
+  const char* base = tile + blk * 32 * Geo<D>::ROWB;
+  const f32x16 zero = {};
+  f32x16 s = mfma(*reinterpret_cast<const bf16x8*>(base + off[0]), b[0], zero);
+#pragma unroll
+  for (int c = 1; c < Geo<D>::NC; ++c)
+    s = mfma(*reinterpret_cast<const bf16x8*>(base + off[c]), b[c], s);
+  return s;
+}
+
+// acc[db] += A^T(block rows 32*blk .. +32, d-block db) . p[j] over the two
+// 16-row chunks j of the block; A is read transposed from a kBothRead tile.
+template <int D>
+__device__ __forceinline__ void tr_mfma(f32x16* acc, const bf16x8* p, const char* tile,
+                                        const int (*tr)[2], int blk) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int db = 0; db < Geo<D>::NDB; ++db) {
+      const char* base = tile + (2 * blk + j) * 16 * Geo<D>::ROWB;
+      acc[db] = mfma(tr_read(base + tr[db][0], base + tr[db][1]), p[j], acc[db]);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void store_acc(uint16_t* row, const f32x16* acc, float mul, int lane) {
+  const int half = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = db * 32 + 8 * g4 + 4 * half;
+      u32x2 w;
+      w[0] = (uint32_t)f2bf(acc[db][4 * g4 + 0] * mul) | ((uint32_t)f2bf(acc[db][4 * g4 + 1] * mul) << 16);
+      w[1] = (uint32_t)f2bf(acc[db][4 * g4 + 2] * mul) | ((uint32_t)f2bf(acc[db][4 * g4 + 3] * mul) << 16);
+      *reinterpret_cast<u32x2*>(row + d0) = w;
+    }
+}
+
+__device__ __forceinline__ uint32_t keep_mask(uint32_t bits, int bit) {
+  return (uint32_t)__builtin_amdgcn_sbfe((int)bits, bit, 1);   // 0 or ~0
+}
+
+// ---- dQ (query-major) --------------------------------------------------------
+
+// LDS: K[2] (rows and transposed) | V[2] (rows) | masks[2]
+template <int D>
+struct QLds {
+  static constexpr int KOFF = 0;
+  static constexpr int VOFF = 2 * Geo<D>::TILEB;
+  static constexpr int MOFF = 4 * Geo<D>::TILEB;
+  static constexpr int SIZE = 4 * Geo<D>::TILEB + 2 * Geo<D>::MBYTES;
+};
+
+template <int D>
+struct QCtx {
+  const HierBwdArgs* a;
+  const char* gk;
+  const char* gv;
+  const int32_t* kv_idx;
+  const uint32_t* kv_mask;
+  const uint32_t* blk;
+  uint32_t k_ss_b, v_ss_b;
+  float c2;
+  int nt, wave, lane;
+  bool active;
+  Copier<D, kBothRead> ck;
+  Copier<D, kRowRead> cv;
+  int krow[Geo<D>::NC], vrow[Geo<D>::NC], ktr[Geo<D>::NDB][2];
+  // rows
+  bf16x8 q[Geo<D>::NC], dov[Geo<D>::NC];
+  f32x16 dq[Geo<D>::NDB];
+  float lse2, delta;
+  int qtok, qframe;
+  bool valid;
+  uint32_t bits;
+};
+
+template <int D, int PAR>
+__device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, char* lds) {
+  constexpr int TB = Geo<D>::TILEB;
+  if (t + 1 < c.nt) {
+    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, lds + QLds<D>::KOFF + (PAR ^ 1) * TB, c.wave);
+    copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, inext, lds + QLds<D>::VOFF + (PAR ^ 1) * TB, c.wave);
+    copy_dwords(c.kv_mask + (t + 1) * kSlab, lds + QLds<D>::MOFF + (PAR ^ 1) * Geo<D>::MBYTES, c.lane);
+    inext = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+  }
+  if (c.active) {
+    const char* ks = lds + QLds<D>::KOFF + PAR * TB;
+    const char* vs = lds + QLds<D>::VOFF + PAR * TB;
+    const uint32_t* mk = reinterpret_cast<const uint32_t*>(lds + QLds<D>::MOFF + PAR * Geo<D>::MBYTES);
+    const bool need = (c.blk[t] & c.bits) != c.bits;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const f32x16 s = row_mfma<D>(c.q, ks, c.krow, kb);
+      const f32x16 dp = row_mfma<D>(c.dov, vs, c.vrow, kb);
+      bf16x8 dsb[2];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        u32x4 w = {~0u, ~0u, ~0u, ~0u};
+        if (need) w = *reinterpret_cast<const u32x4*>(&mk[kb * 32 + 8 * g4 + 4 * (c.lane >> 5)]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g4 + e;
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[i], c.c2, -c.lse2));
+          const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - c.delta)) &
+                                           keep_mask(w[e], c.qframe));
+          dsb[i >> 3][i & 7] = (__bf16)ds;
+        }
+      }
+      tr_mfma<D>(c.dq, dsb, ks, c.ktr, kb);
+    }
+  }
+  wait_copies();
+  __syncthreads();
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int total) {
+  __shared__ __align__(16) char lds[QLds<D>::SIZE];
+  const int G = gridDim.x;
+  const int bid = blockIdx.x;
+  const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
+  if (logical >= total) return;
+  const int head = logical / a.n_items;
+  const int item = logical - head * a.n_items;
+  const int32_t* it = a.tile_items + (int64_t)item * 8;
+
+  QCtx<D> c;
+  c.a = &a;
+  const int tid = threadIdx.x;
+  c.lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qbase = it[0], qstride = it[1], qlen = it[2], row_start = it[3], row_count = it[4];
+  const int kv_off = it[5], kv_cnt = it[6];
+  c.nt = kv_cnt / kSlab;
+  c.active = c.wave * 32 < row_count;
+  c.c2 = a.scale * kLog2e;
+  c.gk = reinterpret_cast<const char*>(a.k + (int64_t)head * a.k_sh);
+  c.gv = reinterpret_cast<const char*>(a.v + (int64_t)head * a.v_sh);
+  c.k_ss_b = (uint32_t)(a.k_ss * 2);
+  c.v_ss_b = (uint32_t)(a.v_ss * 2);
+  c.kv_idx = a.tile_kv_idx + kv_off;
+  c.kv_mask = a.tile_kv_mask + kv_off;
+  c.blk = a.tile_blk_and + kv_off / kSlab;
+  c.ck.init(c.wave, c.lane);
+  c.cv.init(c.wave, c.lane);
+#pragma unroll
+  for (int i = 0; i < Geo<D>::NC; ++i) {
+    c.krow[i] = row_read_off<D, kBothRead>(c.lane, i);
+    c.vrow[i] = row_read_off<D, kRowRead>(c.lane, i);
+  }
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db) {
+    c.ktr[db][0] = tr_read_off<D, kBothRead>(c.lane, db, 0);
+    c.ktr[db][1] = tr_read_off<D, kBothRead>(c.lane, db, 1);
+  }
+
+  // the lane's query row
+  const int r = c.wave * 32 + (c.lane & 31);
+  c.valid = r < row_count;
+  const int ri = row_start + (c.valid ? r : 0);
+  c.qframe = ri / qlen;
+  c.qtok = qbase + c.qframe * qstride + (ri - c.qframe * qlen);
+  c.bits = wave_or(c.valid ? (1u << c.qframe) : 0u);
+  load_row<D>(c.q, a.q + (int64_t)c.qtok * a.q_ss + (int64_t)head * a.q_sh, c.lane);
+  load_row<D>(c.dov, a.dout + (int64_t)c.qtok * a.do_ss + (int64_t)head * a.do_sh, c.lane);
+  {
+    bf16x8 o[Geo<D>::NC];
+    load_row<D>(o, a.o + (int64_t)c.qtok * a.o_ss + (int64_t)head * a.o_sh, c.lane);
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < Geo<D>::NC; ++cc)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        d0 = fmaf((float)c.dov[cc][e], (float)o[cc][e], d0);
+        d1 = fmaf((float)c.dov[cc][e + 1], (float)o[cc][e + 1], d1);
+      }
+    c.delta = pair_sum(d0 + d1);
+  }
+  const int64_t srow = (int64_t)head * a.lse_stride_h + c.qtok;
+  const float lse = a.lse[srow];
+  c.lse2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
+  if (c.valid && c.lane < 32) {
+    a.delta[srow] = c.delta;
+    a.lse2[srow] = c.lse2;
+  }
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c.dq[db][i] = 0.f;
+
+  const int nt = c.nt;
+  if (nt > 0) {
+    const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
+    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, i0, lds + QLds<D>::KOFF, c.wave);
+    copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, i0, lds + QLds<D>::VOFF, c.wave);
+    copy_dwords(c.kv_mask, lds + QLds<D>::MOFF, c.lane);
+    Idx<D> inext = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
+    wait_copies();
+    __syncthreads();
+    int t = 0;
+    for (; t + 1 < nt; t += 2) {
+      dq_tile<D, 0>(c, t, inext, lds);
+      dq_tile<D, 1>(c, t + 1, inext, lds);
+    }
+    if (t < nt) dq_tile<D, 0>(c, t, inext, lds);
+  }
+  if (c.active && c.valid)
+    store_acc<D>(a.dq + (int64_t)c.qtok * a.dq_ss + (int64_t)head * a.dq_sh, c.dq, a.scale, c.lane);
+}
+
+// ---- dK, dV (key-major) ------------------------------------------------------
+
+// LDS: Q[2] | dO[2] (rows and transposed) | per-query dwords[2] x {mask, lse2, delta}
+template <int D>
+struct KLds {
+  static constexpr int QOFF = 0;
+  static constexpr int DOFF = 2 * Geo<D>::TILEB;
+  static constexpr int WOFF = 4 * Geo<D>::TILEB;            // + stage * 3 * MBYTES
+  static constexpr int SIZE = 4 * Geo<D>::TILEB + 6 * Geo<D>::MBYTES;
+};
+
+template <int D>
+struct KCtx {
+  const char* gq;
+  const char* gdo;
+  const float* lse2;     // head row of the workspace
+  const float* delta;
+  const int32_t* q_idx;
+  const uint32_t* q_mask;
+  const uint32_t* blk;
+  uint32_t q_ss_b, do_ss_b;
+  float c2;
+  int nt, wave, lane;
+  bool active;
+  Copier<D, kBothRead> cq;
+  int row[Geo<D>::NC], tr[Geo<D>::NDB][2];
+  // key rows
+  bf16x8 kt[Geo<D>::NC], vt[Geo<D>::NC];
+  f32x16 dk[Geo<D>::NDB], dv[Geo<D>::NDB];
+  int ktok, kframe;
+  bool valid;
+  uint32_t bits;
+};
+
+template <int D>
+__device__ __forceinline__ void kdv_copy(KCtx<D>& c, int t, const Idx<D>& ix, int qtok, char* stage_q,
+                                         char* stage_do, char* stage_w) {
+  copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, ix, stage_q, c.wave);
+  copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, ix, stage_do, c.wave);
+  copy_dwords(c.q_mask + t * kSlab, stage_w, c.lane);
+  __builtin_amdgcn_global_load_lds((gbl_void*)(c.lse2 + qtok), (lds_void*)(stage_w + Geo<D>::MBYTES),
+                                   4, 0, 0);
+  __builtin_amdgcn_global_load_lds((gbl_void*)(c.delta + qtok),
+                                   (lds_void*)(stage_w + 2 * Geo<D>::MBYTES), 4, 0, 0);
+}
+
+template <int D, int PAR>
+__device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int& qnext, char* lds) {
+  constexpr int TB = Geo<D>::TILEB;
+  constexpr int WB = 3 * Geo<D>::MBYTES;
+  if (t + 1 < c.nt) {
+    kdv_copy<D>(c, t + 1, inext, qnext, lds + KLds<D>::QOFF + (PAR ^ 1) * TB,
+                lds + KLds<D>::DOFF + (PAR ^ 1) * TB, lds + KLds<D>::WOFF + (PAR ^ 1) * WB);
+    const int tn = min(t + 2, c.nt - 1);
+    inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
+    qnext = c.q_idx[tn * kSlab + c.lane];
+  }
+  if (c.active) {
+    const char* qs = lds + KLds<D>::QOFF + PAR * TB;
+    const char* ds_ = lds + KLds<D>::DOFF + PAR * TB;
+    const char* ws = lds + KLds<D>::WOFF + PAR * WB;
+    const uint32_t* mk = reinterpret_cast<const uint32_t*>(ws);
+    const float* l2 = reinterpret_cast<const float*>(ws + Geo<D>::MBYTES);
+    const float* dl = reinterpret_cast<const float*>(ws + 2 * Geo<D>::MBYTES);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const f32x16 s = row_mfma<D>(c.kt, qs, c.row, qb);
+      const f32x16 dp = row_mfma<D>(c.vt, ds_, c.row, qb);
+      bf16x8 pb[2], dsb[2];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
+        const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[q0]);
+        const u32x4 lw = *reinterpret_cast<const u32x4*>(&l2[q0]);
+        const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g4 + e;
+          const uint32_t keep = keep_mask(w[e], c.kframe);
+          const float p = __uint_as_float(
+              __float_as_uint(__builtin_amdgcn_exp2f(fmaf(s[i], c.c2, -__uint_as_float(lw[e])))) & keep);
+          const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - __uint_as_float(dw[e]))) & keep);
+          pb[i >> 3][i & 7] = (__bf16)p;
+          dsb[i >> 3][i & 7] = (__bf16)ds;
+        }
+      }
+      tr_mfma<D>(c.dv, pb, ds_, c.tr, qb);
+      tr_mfma<D>(c.dk, dsb, qs, c.tr, qb);
+    }
+  }
+  wait_copies();
+  __syncthreads();
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int total) {
+  __shared__ __align__(16) char lds[KLds<D>::SIZE];
+  const int G = gridDim.x;
+  const int bid = blockIdx.x;
+  const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
+  if (logical >= total) return;
+  const int head = logical / a.n_key_items;
+  const int item = logical - head * a.n_key_items;
+  const int32_t* it = a.key_items + (int64_t)item * 8;
+
+  KCtx<D> c;
+  const int tid = threadIdx.x;
+  c.lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kbase = it[0], kstride = it[1], klen = it[2], row_start = it[3], row_count = it[4];
+  const int q_off = it[5], q_cnt = it[6];
+  c.nt = q_cnt / kSlab;
+  c.active = c.wave * 32 < row_count;
+  c.c2 = a.scale * kLog2e;
+  c.gq = reinterpret_cast<const char*>(a.q + (int64_t)head * a.q_sh);
+  c.gdo = reinterpret_cast<const char*>(a.dout + (int64_t)head * a.do_sh);
+  c.q_ss_b = (uint32_t)(a.q_ss * 2);
+  c.do_ss_b = (uint32_t)(a.do_ss * 2);
+  c.lse2 = a.lse2 + (int64_t)head * a.lse_stride_h;
+  c.delta = a.delta + (int64_t)head * a.lse_stride_h;
+  c.q_idx = a.key_q_idx + q_off;
+  c.q_mask = a.key_q_mask + q_off;
+  c.blk = a.key_blk_and + q_off / kSlab;
+  c.cq.init(c.wave, c.lane);
+#pragma unroll
+  for (int i = 0; i < Geo<D>::NC; ++i) c.row[i] = row_read_off<D, kBothRead>(c.lane, i);
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db) {
+    c.tr[db][0] = tr_read_off<D, kBothRead>(c.lane, db, 0);
+    c.tr[db][1] = tr_read_off<D, kBothRead>(c.lane, db, 1);
+  }
+
+  // the lane's key row
+  const int r = c.wave * 32 + (c.lane & 31);
+  c.valid = r < row_count;
+  const int ri = row_start + (c.valid ? r : 0);
+  c.kframe = ri / klen;
+  c.ktok = kbase + c.kframe * kstride + (ri - c.kframe * klen);
+  c.bits = wave_or(c.valid ? (1u << c.kframe) : 0u);
+  load_row<D>(c.kt, a.k + (int64_t)c.ktok * a.k_ss + (int64_t)head * a.k_sh, c.lane);
+  load_row<D>(c.vt, a.v + (int64_t)c.ktok * a.v_ss + (int64_t)head * a.v_sh, c.lane);
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c.dk[db][i] = c.dv[db][i] = 0.f;
+
+  const int nt = c.nt;
+  if (nt > 0) {
+    const Idx<D> i0 = load_idx<D>(c.q_idx, 0, c.cq.idx_off);
+    kdv_copy<D>(c, 0, i0, c.q_idx[c.lane], lds + KLds<D>::QOFF, lds + KLds<D>::DOFF,
+                lds + KLds<D>::WOFF);
+    const int tn = min(1, nt - 1);
+    Idx<D> inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
+    int qnext = c.q_idx[tn * kSlab + c.lane];
+    wait_copies();
+    __syncthreads();
+    int t = 0;
+    for (; t + 1 < nt; t += 2) {
+      dkdv_tile<D, 0>(c, t, inext, qnext, lds);
+      dkdv_tile<D, 1>(c, t + 1, inext, qnext, lds);
+    }
+    if (t < nt) dkdv_tile<D, 0>(c, t, inext, qnext, lds);
+  }
+  if (c.active && c.valid) {
+    store_acc<D>(a.dk + (int64_t)c.ktok * a.dk_ss + (int64_t)head * a.dk_sh, c.dk, a.scale, c.lane);
+    store_acc<D>(a.dv + (int64_t)c.ktok * a.dv_ss + (int64_t)head * a.dv_sh, c.dv, 1.f, c.lane);
+  }
+}
+
+int64_t span_bytes(int64_t rows, int64_t ss, int64_t sh, int H, int D) {
+  return ((rows > 0 ? rows - 1 : 0) * ss + (int64_t)(H - 1) * sh + D) * 2;
+}
+
+}  // namespace
+
+extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
+  const HierBwdArgs& a = *args;
+  HIER_REQUIRE(a.D == 128 || a.D == 64, HIER_EUNSUPPORTED, "head_dim must be 64 or 128, got %d", a.D);
+  HIER_REQUIRE(a.H >= 1 && a.n_items >= 0 && a.n_key_items >= 0 && a.kv_rows >= 0 && a.q_rows >= 0,
+               HIER_EINVAL, "invalid H=%d n_items=%d n_key_items=%d", a.H, a.n_items, a.n_key_items);
+  HIER_REQUIRE(a.q && a.k && a.v && a.o && a.dout && a.lse && a.delta && a.lse2 && a.dq && a.dk &&
+                   a.dv && a.tile_items && a.tile_kv_idx && a.tile_kv_mask && a.tile_blk_and &&
+                   a.key_items && a.key_q_idx && a.key_q_mask && a.key_blk_and,
+               HIER_EINVAL, "NULL pointer");
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  HIER_REQUIRE(al16(a.q) && al16(a.k) && al16(a.v) && al16(a.o) && al16(a.dout) && al16(a.dq) &&
+                   al16(a.dk) && al16(a.dv) && al16(a.tile_kv_idx) && al16(a.key_q_idx),
+               HIER_EINVAL, "tensors and index lists must be 16-byte aligned");
+  const int64_t st[] = {a.q_ss, a.q_sh, a.k_ss, a.k_sh, a.v_ss, a.v_sh, a.o_ss, a.o_sh,
+                        a.do_ss, a.do_sh, a.dq_ss, a.dq_sh, a.dk_ss, a.dk_sh, a.dv_ss, a.dv_sh};
+  for (int64_t s : st)
+    HIER_REQUIRE(s >= 0 && s % 8 == 0, HIER_EINVAL, "strides must be non-negative multiples of 8");
+  HIER_REQUIRE(span_bytes(a.kv_rows, a.k_ss, a.k_sh, a.H, a.D) <= (1ll << 32) &&
+                   span_bytes(a.kv_rows, a.v_ss, a.v_sh, a.H, a.D) <= (1ll << 32) &&
+                   span_bytes(a.q_rows, a.q_ss, a.q_sh, a.H, a.D) <= (1ll << 32) &&
+                   span_bytes(a.q_rows, a.do_ss, a.do_sh, a.H, a.D) <= (1ll << 32),
+               HIER_EUNSUPPORTED, "Q/K/V/dO views must span at most 4 GiB");
+  const int64_t tq = (int64_t)a.n_items * a.H, tk = (int64_t)a.n_key_items * a.H;
+  HIER_REQUIRE(tq < (1ll << 31) - 8 && tk < (1ll << 31) - 8, HIER_EUNSUPPORTED, "too many work items");
+  hipStream_t s = (hipStream_t)stream;
+  if (tq > 0) {
+    const int grid = (int)((tq + 7) / 8 * 8);
+    if (a.D == 128)
+      hipLaunchKernelGGL(dq_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
+    else
+      hipLaunchKernelGGL(dq_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
+    int rc = hier::check_launch("dq_kernel");
+    if (rc != HIER_OK) return rc;
+  }
+  if (tk > 0) {
+    const int grid = (int)((tk + 7) / 8 * 8);
+    if (a.D == 128)
+      hipLaunchKernelGGL(dkdv_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
+    else
+      hipLaunchKernelGGL(dkdv_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
+    return hier::check_launch("dkdv_kernel");
+  }
+  return HIER_OK;
+}

@@ -16,7 +16,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _capi
-from .metadata import HierTiledBlockLayout, TileList
+from .metadata import HierTiledBlockLayout, TileList, transpose_tiles
 
 
 def _stream(dev) -> C.c_void_p:
@@ -83,6 +83,93 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
         tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr())
     _capi.call("hier_attn_fwd", C.byref(args), _stream(q.device))
     return out
+
+
+def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                            dout: torch.Tensor, lse: torch.Tensor, tiles: TileList, *,
+                            scale: Optional[float] = None,
+                            key_tiles: Optional[TileList] = None):
+    """``hier_attn_bwd``: gradients ``(dq, dk, dv)`` (bf16, shaped like q/k/v) of
+    ``hier_attention_forward(q, k, v, tiles)`` given its output, its ``lse``
+    and the output gradient.  ``tiles`` must be a full-sequence tile list;
+    its key-major counterpart is built (and cached) on first use.
+    """
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
+        if t.dtype != torch.bfloat16:
+            raise NotImplementedError(f"{name} must be bf16, got {t.dtype}")
+        if not t.is_cuda:
+            raise NotImplementedError("hierarchical attention requires a GPU tensor")
+    q3, q_ss, q_sh = _rows_view(q)
+    k3, k_ss, k_sh = _rows_view(k)
+    v3, v_ss, v_sh = _rows_view(v)
+    o3, o_ss, o_sh = _rows_view(out)
+    d3, do_ss, do_sh = _rows_view(dout)
+    H, D = q3.shape[1], q3.shape[2]
+    for t in (k3, v3, o3, d3):
+        if t.shape[1:] != (H, D):
+            raise ValueError("q/k/v/out/dout head shapes differ")
+    if tiles.rows_per_item != 128:
+        raise ValueError("hier_attn_bwd processes work items of up to 128 rows")
+    if k3.shape[0] < tiles.key_extent or v3.shape[0] < tiles.key_extent:
+        raise ValueError(f"K/V hold {k3.shape[0]} rows, the tile list addresses {tiles.key_extent}")
+    if min(q3.shape[0], o3.shape[0], d3.shape[0]) < tiles.row_extent:
+        raise ValueError(f"Q/out/dout hold fewer rows than the tile list addresses ({tiles.row_extent})")
+    if lse.dtype != torch.float32 or lse.dim() != 2 or lse.shape[0] != H or \
+            lse.shape[1] < tiles.row_extent or lse.stride(1) != 1:
+        raise ValueError("lse must be fp32 [H, >=rows] with unit row stride")
+    kt = key_tiles if key_tiles is not None else transpose_tiles(tiles)
+    dev = q.device
+    dq = torch.zeros_like(q3)
+    dk = torch.zeros_like(k3)
+    dv = torch.zeros_like(v3)
+    ws = torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
+    args = _capi.HierBwdArgs(
+        H=H, D=D, n_items=tiles.n_items, n_key_items=kt.n_items,
+        scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
+        kv_rows=min(k3.shape[0], v3.shape[0]), q_rows=min(q3.shape[0], d3.shape[0]), reserved=0,
+        q=q3.data_ptr(), k=k3.data_ptr(), v=v3.data_ptr(), o=o3.data_ptr(), dout=d3.data_ptr(),
+        lse=lse.data_ptr(), delta=ws[0].data_ptr(), lse2=ws[1].data_ptr(),
+        dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(),
+        q_ss=q_ss, q_sh=q_sh, k_ss=k_ss, k_sh=k_sh, v_ss=v_ss, v_sh=v_sh, o_ss=o_ss, o_sh=o_sh,
+        do_ss=do_ss, do_sh=do_sh, dq_ss=dq.stride(0), dq_sh=dq.stride(1), dk_ss=dk.stride(0),
+        dk_sh=dk.stride(1), dv_ss=dv.stride(0), dv_sh=dv.stride(1), lse_stride_h=lse.stride(0),
+        tile_items=tiles.items.data_ptr(), tile_kv_idx=tiles.kv_idx.data_ptr(),
+        tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr(),
+        key_items=kt.items.data_ptr(), key_q_idx=kt.kv_idx.data_ptr(),
+        key_q_mask=kt.kv_mask.data_ptr(), key_blk_and=kt.blk_and.data_ptr())
+    _capi.call("hier_attn_bwd", C.byref(args), _stream(dev))
+    shape = lambda g, like: g.reshape(like.shape) if like.dim() == 4 else g
+    return shape(dq, q), shape(dk, k), shape(dv, v)
+
+
+class HierAttentionFunction(torch.autograd.Function):
+    """Differentiable hierarchical attention: forward ``hier_attn_fwd`` (keeps
+    the LSE), backward ``hier_attn_bwd``.  Inputs ``[S, H, D]`` (or
+    ``[1, S, H, D]``) bf16 over a full-sequence tile list."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, tiles: TileList, scale: Optional[float] = None):
+        q3 = _rows_view(q)[0]
+        H = q3.shape[1]
+        out = torch.zeros_like(q)
+        lse = torch.full((H, q3.shape[0]), float("-inf"), dtype=torch.float32, device=q.device)
+        hier_attention_forward(q, k, v, tiles, out, lse=lse, scale=scale)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.tiles, ctx.scale = tiles, scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = hier_attention_backward(q, k, v, out, dout.contiguous().to(torch.bfloat16),
+                                             lse, ctx.tiles, scale=ctx.scale)
+        return dq, dk, dv, None, None
+
+
+def hier_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tiles: TileList,
+                   scale: Optional[float] = None) -> torch.Tensor:
+    """Autograd-enabled hierarchical attention over a full-sequence tile list."""
+    return HierAttentionFunction.apply(q, k, v, tiles, scale)
 
 
 def hierarchical_tiled_full_sequence_attention(*, roped_q: torch.Tensor, roped_k: torch.Tensor,

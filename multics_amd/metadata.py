@@ -518,6 +518,121 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
 
 
 # --------------------------------------------------------------------------
+# key-major (transposed) tile list for the backward
+# --------------------------------------------------------------------------
+
+def transpose_tiles(tiles: TileList) -> TileList:
+    """Key-major counterpart of a full-sequence tile list (dK / dV pass of
+    ``hier_attn_bwd``).
+
+    In a full-sequence topology every token is a query row of exactly one
+    (block, stream) group and a key of the same group; the forward list of a
+    group is its ordered key list, a concatenation of whole key frames of
+    other groups, each with a bitmask over the group's query frames.  The
+    transposed list of a group is the ordered list of query rows that see any
+    of its key frames, each with a bitmask over the group's key frames: items
+    keep the forward items' row descriptors (now key rows), the lists hold
+    query rows.  Query units are ordered by (query group, query frame); lists
+    are padded to 64 rows with (row 0, mask 0).  Built on the host from the
+    device list once per topology and cached on ``tiles``.
+    """
+    cached = getattr(tiles, "_transposed", None)
+    if cached is not None:
+        return cached
+    dev = tiles.items.device
+    items = tiles.items[:tiles.n_items].cpu().numpy().astype(np.int64)
+    kv_idx = tiles.kv_idx.cpu().numpy().astype(np.int64)
+    kv_mask = tiles.kv_mask.cpu().numpy().astype(np.int64) & 0xFFFFFFFF
+    first = np.nonzero(items[:, 3] == 0)[0]            # first item of each group
+    n_groups = len(first)
+    qbase, qstride, qlen = items[first, 0], items[first, 1], items[first, 2]
+    off, cnt, nfr = items[first, 5], items[first, 6], items[first, 7]
+    grp_of_item = np.repeat(np.arange(n_groups), np.diff(np.append(first, len(items))))
+
+    # token -> (group, row inside the group)
+    S = int(tiles.row_extent)
+    tok_g = np.full(S, -1, np.int64)
+    tok_r = np.full(S, -1, np.int64)
+    for g in range(n_groups):
+        rows = np.arange(int(nfr[g] * qlen[g]))
+        j = rows // qlen[g]
+        toks = qbase[g] + j * qstride[g] + rows - j * qlen[g]
+        if (tok_g[toks] >= 0).any():
+            raise AssertionError("transpose_tiles: a token is a query row of two groups")
+        tok_g[toks] = g
+        tok_r[toks] = rows
+
+    # edges (query group g, key group G, key frame f) -> query-frame mask
+    pos = np.concatenate([np.arange(o, o + c) for o, c in zip(off, cnt)]) if n_groups else \
+        np.zeros(0, np.int64)
+    qg = np.repeat(np.arange(n_groups), cnt)
+    m = kv_mask[pos]
+    live = m != 0
+    pos, qg, m = pos[live], qg[live], m[live]
+    key = kv_idx[pos]
+    if len(key) and (key.max() >= S or (tok_g[key] < 0).any()):
+        raise AssertionError("transpose_tiles: a key is not a query row of any group")
+    kg = tok_g[key]
+    kf = tok_r[key] // qlen[kg]
+    code = (qg * n_groups + kg) * 32 + kf
+    ucode, inv, ucount = np.unique(code, return_inverse=True, return_counts=True)
+    umask = np.zeros(len(ucode), np.int64)
+    np.bitwise_or.at(umask, inv, m)
+    mask_and = np.full(len(ucode), 0xFFFFFFFF, np.int64)
+    np.bitwise_and.at(mask_and, inv, m)
+    e_qg, rest = np.divmod(ucode, n_groups * 32)
+    e_kg, e_kf = np.divmod(rest, 32)
+    if (ucount != qlen[e_kg]).any() or (mask_and != umask).any():
+        raise AssertionError("transpose_tiles: key lists are not whole key frames")
+
+    # per key group: query units (g, j) with a bitmask over key frames
+    nq_max = int(nfr.max(initial=1))
+    lists = []
+    for G in range(n_groups):
+        sel = np.nonzero(e_kg == G)[0]
+        unit_bits = {}
+        for e in sel:
+            g, f, qm = int(e_qg[e]), int(e_kf[e]), int(umask[e])
+            for j in range(nq_max):
+                if (qm >> j) & 1:
+                    unit_bits[(g, j)] = unit_bits.get((g, j), 0) | (1 << f)
+        lists.append(sorted(unit_bits.items()))
+    sizes = np.array([sum(int(qlen[g]) for (g, _), _ in l) for l in lists], np.int64)
+    padded = -(-sizes // TILE_KEYS) * TILE_KEYS
+    new_off = np.concatenate([[0], np.cumsum(padded)])
+    n_q = int(new_off[-1])
+    q_idx = np.zeros(max(n_q, 1), np.int64)
+    q_mask = np.zeros(max(n_q, 1), np.int64)
+    pairs = 0
+    for G, l in enumerate(lists):
+        p = int(new_off[G])
+        for (g, j), bits in l:
+            w = int(qlen[g])
+            q_idx[p:p + w] = qbase[g] + j * qstride[g] + np.arange(w)
+            q_mask[p:p + w] = bits
+            pairs += w * int(qlen[G]) * bin(bits).count("1")
+            p += w
+    if pairs != tiles.logical_pairs:
+        raise AssertionError(f"transpose_tiles: {pairs} pairs, forward list has {tiles.logical_pairs}")
+    blk = q_mask[:max(n_q, TILE_KEYS)].reshape(-1, TILE_KEYS) if n_q else np.zeros((1, TILE_KEYS), np.int64)
+    blk_and = np.bitwise_and.reduce(blk, axis=1) if n_q else np.zeros(1, np.int64)
+    kitems = items.copy()
+    kitems[:, 5] = new_off[grp_of_item]
+    kitems[:, 6] = padded[grp_of_item]
+
+    def to_dev(a):
+        return torch.from_numpy((a & 0xFFFFFFFF).astype(np.uint32).view(np.int32).copy()).to(dev)
+
+    out = TileList(items=torch.from_numpy(kitems.astype(np.int32)).to(dev),
+                   kv_idx=to_dev(q_idx), kv_mask=to_dev(q_mask), blk_and=to_dev(blk_and),
+                   n_items=tiles.n_items, item_ranges=tiles.item_ranges,
+                   logical_pairs=pairs, key_extent=tiles.row_extent, row_extent=tiles.key_extent,
+                   rows_per_item=tiles.rows_per_item)
+    tiles._transposed = out
+    return out
+
+
+# --------------------------------------------------------------------------
 # reference-named entry points with bounded LRU caches
 # --------------------------------------------------------------------------
 

@@ -1,0 +1,125 @@
+"""HIP backward (dQ, dK, dV) against fp32 autograd of the dense-mask oracle.
+
+The reference differentiates its training forward through FlexAttention on the
+dense hierarchical mask (attention.py:322-353, 367-434); the oracle here is the
+same function -- softmax(QK^T / sqrt(D) + mask) V with inactive local-hub rows
+multiplied by 0 -- in fp32 torch autograd on the CPU, from the same bf16
+inputs.  Gradients are bf16; the bound is relative to the gradient's size:
+max-abs <= 2e-2 * max|ref| and mean-abs <= 1e-2 * mean|ref|.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from multics_amd import metadata as M
+from multics_amd.kernels import hier_attention, hier_attention_backward
+from oracle.attention import masked_attention
+from oracle.masks import FullTopology
+from tests.gpu_util import need_gpu, say
+
+pytestmark = pytest.mark.gpu
+REL_MAX, REL_MEAN = 2e-2, 1e-2
+
+
+def _topology(case, rng):
+    name, P, T, L, N, KL, KG, n, W, H, D, direct, kind = case
+    if kind == "membership":
+        mem = rng.random((T, N, P)) < 0.4
+        go = ~mem.any(1) & (rng.random((T, P)) < 0.6)
+        full = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                        direct=direct, membership=mem, global_only=go)
+        return FullTopology(P, T, L, N, KL, KG, n, W, direct, membership=mem, global_only=go), full
+    labels = np.array([[p % N for p in range(P)]] * T)
+    if T >= 2 * n:
+        labels[n:2 * n] = [(p + 1) % N for p in range(P)]
+    active = np.zeros((T, N), dtype=bool)
+    active[np.arange(T)[:, None], labels] = True
+    if kind == "inactive":
+        active[:, -1] = False
+    full = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                    direct=direct, labels=labels, active=active)
+    return FullTopology(P, T, L, N, KL, KG, n, W, direct, labels=labels, active=active), full
+
+
+CASES = [
+    # name, P, T, L, N, KL, KG, n, W, H, D, direct, kind
+    ("d128_w4", 4, 6, 20, 2, 5, 6, 3, 4, 2, 128, True, "labels"),
+    ("d128_nodirect", 4, 6, 20, 2, 5, 6, 3, -1, 2, 128, False, "labels"),
+    ("d64_c1", 4, 3, 64, 2, 1, 1, 3, 21, 2, 64, True, "labels"),
+    ("d128_inactive", 3, 6, 37, 3, 2, 3, 2, 4, 2, 128, True, "inactive"),
+    ("d128_membership", 6, 6, 24, 3, 2, 3, 3, 4, 2, 128, True, "membership"),
+]
+
+
+def _check(name, got, ref):
+    err = (got.float().cpu() - ref).abs()
+    scale_max = ref.abs().max().item()
+    scale_mean = ref.abs().mean().item()
+    say(f"  {name}: max-abs {err.max().item():.3e} (ref max {scale_max:.3e}) "
+        f"mean-abs {err.mean().item():.3e} (ref mean {scale_mean:.3e})")
+    assert torch.isfinite(got.float()).all()
+    assert err.max().item() <= REL_MAX * scale_max + 1e-6
+    assert err.mean().item() <= REL_MEAN * scale_mean + 1e-7
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_backward_matches_oracle_autograd(case):
+    need_gpu()
+    rng = np.random.default_rng(11)
+    topo, full = _topology(case, rng)
+    H, D = case[9], case[10]
+    say("backward", case[0], "S", topo.S)
+    g = torch.Generator().manual_seed(5)
+    q, k, v = [(torch.randn(topo.S, H, D, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3)]
+    dout = torch.randn(topo.S, H, D, generator=g).to(torch.bfloat16)
+    tiles = M.build(full, "cuda").tiles
+
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    out = hier_attention(qd, kd, vd, tiles)
+    out.backward(dout.cuda())
+    torch.cuda.synchronize()
+
+    qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))
+    ref = masked_attention(qf, kf, vf, topo)
+    ref.backward(dout.float())
+    _check("out", out.detach(), ref.detach())
+    _check("dq", qd.grad, qf.grad)
+    _check("dk", kd.grad, kf.grad)
+    _check("dv", vd.grad, vf.grad)
+
+
+def test_backward_is_deterministic():
+    need_gpu()
+    rng = np.random.default_rng(2)
+    topo, full = _topology(CASES[0], rng)
+    H, D = 2, 128
+    g = torch.Generator().manual_seed(9)
+    q, k, v, dout = [torch.randn(topo.S, H, D, generator=g).to(torch.bfloat16).cuda() for _ in range(4)]
+    tiles = M.build(full, "cuda").tiles
+    say("backward determinism")
+    res = []
+    for _ in range(2):
+        qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+        hier_attention(qd, kd, vd, tiles).backward(dout)
+        res.append(torch.cat([qd.grad, kd.grad, vd.grad]))
+    torch.cuda.synchronize()
+    assert torch.equal(res[0], res[1])
+
+
+def test_backward_argument_errors():
+    need_gpu()
+    rng = np.random.default_rng(2)
+    topo, full = _topology(CASES[0], rng)
+    tiles = M.build(full, "cuda").tiles
+    H, D = 2, 128
+    x = torch.zeros(topo.S, H, D, dtype=torch.bfloat16, device="cuda")
+    lse = torch.zeros(H, topo.S, device="cuda")
+    with pytest.raises(NotImplementedError):
+        hier_attention_backward(x.float(), x, x, x, x, lse, tiles)
+    with pytest.raises(ValueError):
+        hier_attention_backward(x, x[:-1], x, x, x, lse, tiles)
+    with pytest.raises(ValueError):
+        hier_attention_backward(x, x, x, x, x, lse.double(), tiles)
