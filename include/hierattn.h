@@ -228,6 +228,22 @@ typedef struct HierBwdArgs {
   const int32_t* key_q_idx;        /* describe key rows, lists hold query rows */
   const uint32_t* key_q_mask;      /* bit f: the query sees key frame f        */
   const uint32_t* key_blk_and;
+  /* Optional membership STE (n_ste_items > 0): a query-major list holding   */
+  /* only the keys whose edge to the query row is gated by one membership    */
+  /* bit -- local-hub keys of group g for player-p rows, player-p keys for   */
+  /* local-hub rows of group g, both at the query frame -- with per key the  */
+  /* class c (g for player rows, p for local-hub rows).  The pass adds      */
+  /* dS = P (dP - delta) over each row's keys of class c into                */
+  /* ste_partial[h][row][c] (fp32, c < ste_classes <= 16, zero-initialised */
+  /* by the caller); rows of other items are untouched.                     */
+  int32_t n_ste_items;
+  int32_t ste_classes;
+  const int32_t* ste_items;
+  const int32_t* ste_kv_idx;
+  const uint32_t* ste_kv_mask;
+  const int32_t* ste_kv_class;
+  float* ste_partial;              /* [H][ste_rows][16]                        */
+  int64_t ste_stride_h;            /* elements between heads of ste_partial    */
 } HierBwdArgs;
 
 int hier_attn_bwd(const HierBwdArgs* args, void* stream);

@@ -82,7 +82,11 @@ class HierBwdArgs(C.Structure):
                                    "do_ss", "do_sh", "dq_ss", "dq_sh", "dk_ss", "dk_sh", "dv_ss",
                                    "dv_sh", "lse_stride_h")] + \
                [(n, vp) for n in ("tile_items", "tile_kv_idx", "tile_kv_mask", "tile_blk_and",
-                                  "key_items", "key_q_idx", "key_q_mask", "key_blk_and")]
+                                  "key_items", "key_q_idx", "key_q_mask", "key_blk_and")] + \
+               [("n_ste_items", i32), ("ste_classes", i32)] + \
+               [(n, vp) for n in ("ste_items", "ste_kv_idx", "ste_kv_mask", "ste_kv_class",
+                                  "ste_partial")] + \
+               [("ste_stride_h", i64)]
 
 
 EXPORTS = {

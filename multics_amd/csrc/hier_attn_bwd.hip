@@ -427,6 +427,113 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int to
   }
 }
 
+// ---- membership STE partial sums (query-major, gated keys only) -------------
+
+constexpr int kSteClasses = 16;
+
+// LDS: K[2] | V[2] (rows) | masks[2] | classes[2] | per-wave row sums
+template <int D>
+struct SLds {
+  static constexpr int KOFF = 0;
+  static constexpr int VOFF = 2 * Geo<D>::TILEB;
+  static constexpr int MOFF = 4 * Geo<D>::TILEB;
+  static constexpr int COFF = MOFF + 2 * Geo<D>::MBYTES;
+  static constexpr int AOFF = COFF + 2 * Geo<D>::MBYTES;
+  static constexpr int SIZE = AOFF + kWaves * 32 * kSteClasses * 4;
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int total) {
+  __shared__ __align__(16) char lds[SLds<D>::SIZE];
+  const int G = gridDim.x;
+  const int bid = blockIdx.x;
+  const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
+  if (logical >= total) return;
+  const int head = logical / a.n_ste_items;
+  const int item = logical - head * a.n_ste_items;
+  const int32_t* it = a.ste_items + (int64_t)item * 8;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qbase = it[0], qstride = it[1], qlen = it[2], row_start = it[3], row_count = it[4];
+  const int kv_off = it[5], kv_cnt = it[6];
+  const int nt = kv_cnt / kSlab;
+  const bool active = wave * 32 < row_count;
+  const float c2 = a.scale * kLog2e;
+  const char* gk = reinterpret_cast<const char*>(a.k + (int64_t)head * a.k_sh);
+  const char* gv = reinterpret_cast<const char*>(a.v + (int64_t)head * a.v_sh);
+  const uint32_t k_ss_b = (uint32_t)(a.k_ss * 2), v_ss_b = (uint32_t)(a.v_ss * 2);
+  const int32_t* kv_idx = a.ste_kv_idx + kv_off;
+  const uint32_t* kv_mask = a.ste_kv_mask + kv_off;
+  const int32_t* kv_cls = a.ste_kv_class + kv_off;
+  Copier<D, kRowRead> cp;
+  cp.init(wave, lane);
+  int roff[Geo<D>::NC];
+#pragma unroll
+  for (int i = 0; i < Geo<D>::NC; ++i) roff[i] = row_read_off<D, kRowRead>(lane, i);
+
+  float* acc = reinterpret_cast<float*>(lds + SLds<D>::AOFF) + (wave * 32 + (lane & 31)) * kSteClasses;
+  if (lane < 32)
+#pragma unroll
+    for (int cc = 0; cc < kSteClasses; ++cc) acc[cc] = 0.f;
+
+  const int r = wave * 32 + (lane & 31);
+  const bool valid = r < row_count;
+  const int ri = row_start + (valid ? r : 0);
+  const int qframe = ri / qlen;
+  const int qtok = qbase + qframe * qstride + (ri - qframe * qlen);
+  bf16x8 q[Geo<D>::NC], dov[Geo<D>::NC];
+  load_row<D>(q, a.q + (int64_t)qtok * a.q_ss + (int64_t)head * a.q_sh, lane);
+  load_row<D>(dov, a.dout + (int64_t)qtok * a.do_ss + (int64_t)head * a.do_sh, lane);
+  const int64_t srow = (int64_t)head * a.lse_stride_h + qtok;
+  const float lse2 = a.lse2[srow], delta = a.delta[srow];
+
+  for (int t = 0; t < nt; ++t) {
+    const int par = t & 1;
+    char* ks = lds + SLds<D>::KOFF + par * Geo<D>::TILEB;
+    char* vs = lds + SLds<D>::VOFF + par * Geo<D>::TILEB;
+    char* ms = lds + SLds<D>::MOFF + par * Geo<D>::MBYTES;
+    char* cs = lds + SLds<D>::COFF + par * Geo<D>::MBYTES;
+    const Idx<D> ix = load_idx<D>(kv_idx, t, cp.idx_off);
+    copy_tile<D, kRowRead>(gk, k_ss_b, cp, ix, ks, wave);
+    copy_tile<D, kRowRead>(gv, v_ss_b, cp, ix, vs, wave);
+    copy_dwords(kv_mask + t * kSlab, ms, lane);
+    copy_dwords(kv_cls + t * kSlab, cs, lane);
+    wait_copies();
+    __syncthreads();
+    if (active) {
+      const uint32_t* mk = reinterpret_cast<const uint32_t*>(ms);
+      const int32_t* ck = reinterpret_cast<const int32_t*>(cs);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const f32x16 s = row_mfma<D>(q, ks, roff, kb);
+        const f32x16 dp = row_mfma<D>(dov, vs, roff, kb);
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int k0 = kb * 32 + 8 * g4 + 4 * (lane >> 5);
+          const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[k0]);
+          const u32x4 cl = *reinterpret_cast<const u32x4*>(&ck[k0]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * g4 + e;
+            const float p = __builtin_amdgcn_exp2f(fmaf(s[i], c2, -lse2));
+            const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - delta)) &
+                                             keep_mask(w[e], qframe));
+            if (valid) atomicAdd(&acc[cl[e] & (kSteClasses - 1)], ds);
+          }
+        }
+      }
+    }
+    __syncthreads();   // stage par is rewritten two tiles later; keep it simple
+  }
+  if (active && valid && lane < 32) {
+    float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)qtok * kSteClasses;
+#pragma unroll
+    for (int cc = 0; cc < kSteClasses; ++cc)
+      if (cc < a.ste_classes) dst[cc] = acc[cc];
+  }
+}
+
 int64_t span_bytes(int64_t rows, int64_t ss, int64_t sh, int H, int D) {
   return ((rows > 0 ? rows - 1 : 0) * ss + (int64_t)(H - 1) * sh + D) * 2;
 }
@@ -457,6 +564,17 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
                    span_bytes(a.q_rows, a.q_ss, a.q_sh, a.H, a.D) <= (1ll << 32) &&
                    span_bytes(a.q_rows, a.do_ss, a.do_sh, a.H, a.D) <= (1ll << 32),
                HIER_EUNSUPPORTED, "Q/K/V/dO views must span at most 4 GiB");
+  HIER_REQUIRE(a.n_ste_items >= 0, HIER_EINVAL, "n_ste_items must be >= 0");
+  if (a.n_ste_items > 0) {
+    HIER_REQUIRE(a.ste_items && a.ste_kv_idx && a.ste_kv_mask && a.ste_kv_class && a.ste_partial &&
+                     al16(a.ste_kv_idx) && al16(a.ste_kv_mask) && al16(a.ste_kv_class),
+                 HIER_EINVAL, "membership STE: NULL or misaligned list");
+    HIER_REQUIRE(a.ste_classes >= 1 && a.ste_classes <= kSteClasses, HIER_EUNSUPPORTED,
+                 "membership STE supports 1..%d classes (groups / players), got %d", kSteClasses,
+                 a.ste_classes);
+    HIER_REQUIRE((int64_t)a.n_ste_items * a.H < (1ll << 31) - 8, HIER_EUNSUPPORTED,
+                 "too many work items");
+  }
   const int64_t tq = (int64_t)a.n_items * a.H, tk = (int64_t)a.n_key_items * a.H;
   HIER_REQUIRE(tq < (1ll << 31) - 8 && tk < (1ll << 31) - 8, HIER_EUNSUPPORTED, "too many work items");
   hipStream_t s = (hipStream_t)stream;
@@ -475,7 +593,17 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
       hipLaunchKernelGGL(dkdv_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
     else
       hipLaunchKernelGGL(dkdv_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
-    return hier::check_launch("dkdv_kernel");
+    int rc = hier::check_launch("dkdv_kernel");
+    if (rc != HIER_OK) return rc;
+  }
+  const int64_t ts = (int64_t)a.n_ste_items * a.H;
+  if (a.n_ste_items > 0) {
+    const int grid = (int)((ts + 7) / 8 * 8);
+    if (a.D == 128)
+      hipLaunchKernelGGL(ste_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)ts);
+    else
+      hipLaunchKernelGGL(ste_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)ts);
+    return hier::check_launch("ste_kernel");
   }
   return HIER_OK;
 }

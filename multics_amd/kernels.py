@@ -16,7 +16,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _capi
-from .metadata import HierTiledBlockLayout, TileList, transpose_tiles
+from .metadata import HierTiledBlockLayout, TileList, ste_tiles, transpose_tiles
 
 
 def _stream(dev) -> C.c_void_p:
@@ -85,14 +85,22 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
     return out
 
 
+STE_CLASSES = 16
+
+
 def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                             dout: torch.Tensor, lse: torch.Tensor, tiles: TileList, *,
                             scale: Optional[float] = None,
-                            key_tiles: Optional[TileList] = None):
+                            key_tiles: Optional[TileList] = None,
+                            ste_geometry: Optional[tuple] = None):
     """``hier_attn_bwd``: gradients ``(dq, dk, dv)`` (bf16, shaped like q/k/v) of
     ``hier_attention_forward(q, k, v, tiles)`` given its output, its ``lse``
     and the output gradient.  ``tiles`` must be a full-sequence tile list;
     its key-major counterpart is built (and cached) on first use.
+
+    With ``ste_geometry=(P, T, L, N, KL)`` a fourth result is returned: the
+    sum of dS = P (dP - delta) over the membership-gated edges of every bit,
+    as an fp32 ``[T, N, P]`` tensor (see ``membership_grad``).
     """
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
         if t.dtype != torch.bfloat16:
@@ -123,6 +131,13 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     dk = torch.zeros_like(k3)
     dv = torch.zeros_like(v3)
     ws = torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
+    ste = None
+    if ste_geometry is not None:
+        P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
+        if max(P_, N_) > STE_CLASSES:
+            raise NotImplementedError(f"membership STE supports up to {STE_CLASSES} players / groups")
+        ste = ste_tiles(tiles, P=P_, T=T_, L=L_, N=N_, KL=KL_)
+        partial = torch.zeros((H, tiles.row_extent, STE_CLASSES), dtype=torch.float32, device=dev)
     args = _capi.HierBwdArgs(
         H=H, D=D, n_items=tiles.n_items, n_key_items=kt.n_items,
         scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
@@ -137,39 +152,85 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr(),
         key_items=kt.items.data_ptr(), key_q_idx=kt.kv_idx.data_ptr(),
         key_q_mask=kt.kv_mask.data_ptr(), key_blk_and=kt.blk_and.data_ptr())
+    if ste is not None:
+        sl, scls = ste
+        args.n_ste_items, args.ste_classes = sl.n_items, STE_CLASSES
+        args.ste_items, args.ste_kv_idx = sl.items.data_ptr(), sl.kv_idx.data_ptr()
+        args.ste_kv_mask, args.ste_kv_class = sl.kv_mask.data_ptr(), scls.data_ptr()
+        args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
     _capi.call("hier_attn_bwd", C.byref(args), _stream(dev))
     shape = lambda g, like: g.reshape(like.shape) if like.dim() == 4 else g
-    return shape(dq, q), shape(dk, k), shape(dv, v)
+    res = (shape(dq, q), shape(dk, k), shape(dv, v))
+    if ste_geometry is None:
+        return res
+    P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
+    a0 = P_ * T_ * L_
+    g_player = partial[:, :a0].reshape(H, P_, T_, L_, STE_CLASSES).sum(dim=(0, 3))[..., :N_]
+    g_local = partial[:, a0:a0 + T_ * N_ * KL_].reshape(H, T_, N_, KL_, STE_CLASSES)
+    g_local = g_local.sum(dim=(0, 3))[..., :P_]
+    return res + (g_player.permute(1, 2, 0) + g_local,)
+
+
+def membership_grad(logits: torch.Tensor, gated_ds: torch.Tensor) -> torch.Tensor:
+    """Straight-through gradient of soft membership logits ``[T, N, P]``.
+
+    The forward uses the hard membership ``logits > 0``.  Each edge whose
+    existence depends on one membership bit (t, g, p) -- player p's row at
+    frame t to a local-hub key of group g, or group g's hub row at frame t to a
+    key of player p -- carries the surrogate logit bias
+    ``sigmoid(logit) - stopgrad(sigmoid(logit))`` (zero in value), so
+    ``dL/dlogit = sigmoid'(logit) * sum of dS over those edges`` with
+    dS = dL/d(scaled score) = P (dP - delta).  Edges that are off have P = 0
+    and contribute nothing; same-group player-to-player edges depend on two
+    players' bits jointly and carry no surrogate bias.
+    """
+    sig = torch.sigmoid(logits.float())
+    return (sig * (1.0 - sig) * gated_ds.to(sig.device)).to(logits.dtype)
 
 
 class HierAttentionFunction(torch.autograd.Function):
     """Differentiable hierarchical attention: forward ``hier_attn_fwd`` (keeps
     the LSE), backward ``hier_attn_bwd``.  Inputs ``[S, H, D]`` (or
-    ``[1, S, H, D]``) bf16 over a full-sequence tile list."""
+    ``[1, S, H, D]``) bf16 over a full-sequence tile list; optional membership
+    logits ``[T, N, P]`` receive the straight-through gradient of
+    ``membership_grad`` (their hard value must be the membership the tile list
+    was built from; ``ste_geometry = (P, T, L, N, KL)``)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, tiles: TileList, scale: Optional[float] = None):
+    def forward(ctx, q, k, v, tiles: TileList, scale: Optional[float] = None,
+                logits: Optional[torch.Tensor] = None, ste_geometry: Optional[tuple] = None):
         q3 = _rows_view(q)[0]
         H = q3.shape[1]
         out = torch.zeros_like(q)
         lse = torch.full((H, q3.shape[0]), float("-inf"), dtype=torch.float32, device=q.device)
         hier_attention_forward(q, k, v, tiles, out, lse=lse, scale=scale)
-        ctx.save_for_backward(q, k, v, out, lse)
-        ctx.tiles, ctx.scale = tiles, scale
+        if logits is not None:
+            ctx.save_for_backward(q, k, v, out, lse, logits)
+        else:
+            ctx.save_for_backward(q, k, v, out, lse)
+        ctx.tiles, ctx.scale, ctx.ste_geometry = tiles, scale, ste_geometry
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = hier_attention_backward(q, k, v, out, dout.contiguous().to(torch.bfloat16),
-                                             lse, ctx.tiles, scale=ctx.scale)
-        return dq, dk, dv, None, None
+        saved = ctx.saved_tensors
+        q, k, v, out, lse = saved[:5]
+        logits = saved[5] if len(saved) > 5 else None
+        want_ste = logits is not None and ctx.needs_input_grad[5]
+        res = hier_attention_backward(q, k, v, out, dout.contiguous().to(torch.bfloat16), lse,
+                                      ctx.tiles, scale=ctx.scale,
+                                      ste_geometry=ctx.ste_geometry if want_ste else None)
+        dlogits = membership_grad(logits, res[3]) if want_ste else None
+        return res[0], res[1], res[2], None, None, dlogits, None
 
 
 def hier_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tiles: TileList,
-                   scale: Optional[float] = None) -> torch.Tensor:
+                   scale: Optional[float] = None, *, membership_logits: Optional[torch.Tensor] = None,
+                   ste_geometry: Optional[tuple] = None) -> torch.Tensor:
     """Autograd-enabled hierarchical attention over a full-sequence tile list."""
-    return HierAttentionFunction.apply(q, k, v, tiles, scale)
+    if membership_logits is not None and ste_geometry is None:
+        raise ValueError("membership_logits need ste_geometry=(P, T, L, N, KL)")
+    return HierAttentionFunction.apply(q, k, v, tiles, scale, membership_logits, ste_geometry)
 
 
 def hierarchical_tiled_full_sequence_attention(*, roped_q: torch.Tensor, roped_k: torch.Tensor,

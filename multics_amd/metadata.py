@@ -632,6 +632,74 @@ def transpose_tiles(tiles: TileList) -> TileList:
     return out
 
 
+def ste_tiles(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
+    """Query-major list of the membership-gated edges of a full-sequence tile
+    list (the membership STE pass of ``hier_attn_bwd``).
+
+    An edge's existence depends on exactly one membership bit (t, g, p) when it
+    joins player p's row at frame t to a local-hub key of group g, or group g's
+    local-hub row at frame t to a key of player p (membership at the query
+    frame, hier_masks.py:593-594, 611-612).  The list keeps, per player group,
+    its local-hub keys and, per local-hub group, its player keys, with the
+    forward masks and per key the class (g for player rows, p for hub rows);
+    other groups are dropped.  Returns ``(TileList, kv_class)`` or None when no
+    edge is gated; cached on ``tiles``.
+    """
+    key = (P, T, L, N, KL)
+    cache = getattr(tiles, "_ste", None)
+    if cache is not None and cache[0] == key:
+        return cache[1]
+    a0, g0 = P * T * L, P * T * L + T * N * KL
+    dev = tiles.items.device
+    items = tiles.items[:tiles.n_items].cpu().numpy().astype(np.int64)
+    kv_idx = tiles.kv_idx.cpu().numpy().astype(np.int64)
+    kv_mask = tiles.kv_mask.cpu().numpy().astype(np.int64) & 0xFFFFFFFF
+    first = np.nonzero(items[:, 3] == 0)[0]
+    ends = np.append(first[1:], len(items))
+    out_items, idx_parts, mask_parts, cls_parts = [], [], [], []
+    cursor = 0
+    for f0, f1 in zip(first, ends):
+        qb, off, cnt = int(items[f0, 0]), int(items[f0, 5]), int(items[f0, 6])
+        if qb >= g0 or cnt == 0:
+            continue
+        k = kv_idx[off:off + cnt]
+        m = kv_mask[off:off + cnt]
+        if qb < a0:                      # player rows: local-hub keys, class = group
+            sel = (m != 0) & (k >= a0) & (k < g0)
+            cls = ((k - a0) // max(KL, 1)) % max(N, 1)
+        else:                            # local-hub rows: player keys, class = player
+            sel = (m != 0) & (k < a0)
+            cls = k // (T * L)
+        if not sel.any():
+            continue
+        n = int(sel.sum())
+        pad = -n % TILE_KEYS
+        idx_parts += [k[sel], np.zeros(pad, np.int64)]
+        mask_parts += [m[sel], np.zeros(pad, np.int64)]
+        cls_parts += [cls[sel], np.zeros(pad, np.int64)]
+        for it in range(f0, f1):
+            row = items[it].copy()
+            row[5], row[6] = cursor, n + pad
+            out_items.append(row)
+        cursor += n + pad
+    if not out_items:
+        res = None
+    else:
+        def to_dev(a):
+            return torch.from_numpy((a & 0xFFFFFFFF).astype(np.uint32).view(np.int32).copy()).to(dev)
+        idx = np.concatenate(idx_parts)
+        msk = np.concatenate(mask_parts)
+        blk = np.bitwise_and.reduce(msk.reshape(-1, TILE_KEYS), axis=1)
+        lst = TileList(items=torch.from_numpy(np.asarray(out_items, np.int32)).to(dev),
+                       kv_idx=to_dev(idx), kv_mask=to_dev(msk), blk_and=to_dev(blk),
+                       n_items=len(out_items), item_ranges=(), logical_pairs=0,
+                       key_extent=tiles.key_extent, row_extent=tiles.row_extent,
+                       rows_per_item=tiles.rows_per_item)
+        res = (lst, to_dev(np.concatenate(cls_parts)))
+    tiles._ste = (key, res)
+    return res
+
+
 # --------------------------------------------------------------------------
 # reference-named entry points with bounded LRU caches
 # --------------------------------------------------------------------------

@@ -123,3 +123,37 @@ def test_backward_argument_errors():
         hier_attention_backward(x, x[:-1], x, x, x, lse, tiles)
     with pytest.raises(ValueError):
         hier_attention_backward(x, x, x, x, x, lse.double(), tiles)
+
+
+def test_membership_ste_gradient_matches_oracle():
+    """Soft membership logits ~ N(0, 1): hard forward on logits > 0, the
+    straight-through logit gradient of oracle/ste.py (fp32 autograd)."""
+    need_gpu()
+    from oracle.ste import ste_attention
+    rng = np.random.default_rng(21)
+    P, T, L, N, KL, KG, n, W, H, D = 4, 6, 24, 2, 5, 6, 3, 4, 2, 128
+    logits = torch.from_numpy(rng.standard_normal((T, N, P))).float()
+    mem = (logits > 0).numpy()
+    go = ~mem.any(1)
+    topo = FullTopology(P, T, L, N, KL, KG, n, W, True, membership=mem, global_only=go)
+    full = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W, direct=True,
+                                    membership=mem, global_only=go)
+    g = torch.Generator().manual_seed(4)
+    q, k, v = [(torch.randn(topo.S, H, D, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3)]
+    dout = torch.randn(topo.S, H, D, generator=g).to(torch.bfloat16)
+    tiles = M.build(full, "cuda").tiles
+    say("membership STE", topo.S)
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    lg = logits.cuda().requires_grad_(True)
+    out = hier_attention(qd, kd, vd, tiles, membership_logits=lg, ste_geometry=(P, T, L, N, KL))
+    out.backward(dout.cuda())
+    torch.cuda.synchronize()
+    qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))
+    lf = logits.clone().requires_grad_(True)
+    ref = ste_attention(qf, kf, vf, topo, lf)
+    ref.backward(dout.float())
+    _check("dq", qd.grad, qf.grad)
+    _check("dk", kd.grad, kf.grad)
+    _check("dv", vd.grad, vf.grad)
+    _check("dlogits", lg.grad, lf.grad)
+    assert (lf.grad != 0).any()
