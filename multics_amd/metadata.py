@@ -799,6 +799,24 @@ def build_hier_tiled_full_sequence_layouts(*, device, num_players, num_frames, n
     return hit
 
 
+def full_sequence_tiles(*, device, P, T, L, N, KL, KG, n, window, direct, labels=None, active=None,
+                        membership=None, global_only=None, no_local=False) -> TileList:
+    """Tile list of a full-sequence topology (labels or membership form), kept in
+    the same bounded LRU as the tiled layouts (WAN_HIER_TILED_LAYOUT_CACHE_SIZE)."""
+    key = ("tiles", str(torch.device(device)), P, T, L, N, KL, KG, n, window, bool(direct),
+           bool(no_local), _freeze(labels), _freeze(active), _freeze(membership),
+           _freeze(global_only))
+    hit = _lru_get(_LAYOUT_CACHE, key)
+    if hit is None:
+        topo = full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=window,
+                                      direct=direct, labels=labels, active=active,
+                                      membership=membership, global_only=global_only,
+                                      no_local=no_local)
+        hit = build(topo, device).tiles
+        _lru_put(_LAYOUT_CACHE, key, hit, "WAN_HIER_TILED_LAYOUT_CACHE_SIZE", "2")
+    return hit
+
+
 def build_hier_tiled_cached_layout(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn,
                                    agent_frame_lists, local_frame_lists, global_frame_list,
                                    local_active_frames, labels, q_active, direct_player):

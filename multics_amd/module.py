@@ -1,0 +1,247 @@
+"""Drop-in ``SelfAttention`` for the Wan-DiT blocks, on the HIP kernels.
+
+Same constructor, parameters (state-dict keys ``q, k, v, o, norm_q, norm_k,
+cam_q, cam_k``), mutable attributes and call signatures as the reference module
+(multics/models/attention.py:255-442):
+
+* ``forward_hier_tiled_ste(x, freqs, mask, *, group_labels, active_group, ...)``
+  -- the training / full-sequence hierarchical forward.  The reference takes the
+  Tiled128 value and the FlexAttention Jacobian (attention.py:367-434); here
+  value and Jacobian both come from the HIP kernels (``hier_attn_fwd`` /
+  ``hier_attn_bwd``), so the straight-through combination is the identity.
+  ``mask`` (a Flex BlockMask in the reference) is accepted and not needed: the
+  tile list comes from the group arguments.
+* ``forward_hier_membership(...)`` -- the same for membership / global_only
+  topologies, optionally with soft membership logits that receive the
+  straight-through gradient (``kernels.membership_grad``).
+* ``forward(x, freqs, mask=None, cam_tokens=None)`` -- dense boolean masks go
+  to ``scaled_dot_product_attention`` as in the reference (attention.py:39-54).
+
+Q/K/V projection: with autograd active, torch ops with the reference's
+rounding points (camera adapter, RMSNorm in fp32, RoPE in float64); without
+autograd, the fused HIP prologue (camera + RMSNorm + gain + RoPE in one pass).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import metadata as M
+from .kernels import hier_attention, hier_attention_forward, qkv_prologue
+from .rope import freqs_to_cos_sin
+
+
+class RMSNorm(nn.Module):
+    """attention.py:231-242: normalise in fp32, cast back, times the gain."""
+
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)).to(x.dtype) * \
+            self.weight
+
+
+class CompatibleLinear(nn.Linear):
+    """nn.Linear with the reference's extra constructor arguments
+    (compatible_linear.py:38-50).  The reference zero-pads the input dimension
+    to ``input_alignment`` for one CUDA GEMM path; padding with zeros does not
+    change the product, so this is a plain linear layer."""
+
+    def __init__(self, in_features, out_features, bias=True, *, output_chunk_size=0,
+                 input_alignment=1, device=None, dtype=None):
+        if output_chunk_size < 0 or input_alignment < 1:
+            raise ValueError("output_chunk_size must be >= 0 and input_alignment >= 1")
+        super().__init__(in_features, out_features, bias=bias, device=device, dtype=dtype)
+        self.output_chunk_size = output_chunk_size
+        self.input_alignment = input_alignment
+
+
+def rope_apply(x: torch.Tensor, freqs: torch.Tensor, num_heads: int) -> torch.Tensor:
+    """rope.py:248-254: rotate channel pairs by complex ``freqs`` [S, 1, D/2] in
+    float64 and cast back to the input dtype."""
+    b, s, dim = x.shape
+    xc = torch.view_as_complex(x.to(torch.float64).reshape(b, s, num_heads, -1, 2))
+    return torch.view_as_real(xc * freqs.to(x.device)).flatten(2).to(x.dtype)
+
+
+class SelfAttention(nn.Module):
+    def __init__(self, dim: int, num_heads: int, eps: float = 1e-06):
+        super().__init__()
+        self.dim = dim
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.q = nn.Linear(dim, dim)
+        self.k = nn.Linear(dim, dim)
+        self.v = nn.Linear(dim, dim)
+        self.o = nn.Linear(dim, dim)
+        self.norm_q = RMSNorm(dim, eps=eps)
+        self.norm_k = RMSNorm(dim, eps=eps)
+        self.eps = eps
+        self.sink_size = 0
+        self.local_attn_size = 6
+        self.num_frame_per_block = 7
+        self.attn_impl = "sdpa"
+        self.max_attention_size = self.local_attn_size * 3072
+        self.hier_no_local_hub = False
+        self.cam_dim = None
+        self.cam_q = None
+        self.cam_k = None
+        self.cam_dropout_p = 0.0
+
+    # ---- camera adapters (attention.py:278-320) ---------------------------------
+
+    def enable_camera_pose_qk(self, cam_dim: int, dropout_p: float = 0.1):
+        """Zero-initialised, bias-free camera adapters on Q and K."""
+        cam_dim = int(cam_dim)
+        dropout_p = float(dropout_p)
+        if not 0.0 <= dropout_p < 1.0:
+            raise ValueError(f"camera dropout_p must be in [0,1), got {dropout_p}")
+        if self.cam_q is not None and self.cam_dim == cam_dim:
+            self.cam_dropout_p = dropout_p
+            return
+        device, dtype = self.q.weight.device, self.q.weight.dtype
+        self.cam_dim = cam_dim
+        self.cam_dropout_p = dropout_p
+        self.cam_q = CompatibleLinear(cam_dim, self.dim, bias=False, input_alignment=16).to(
+            device=device, dtype=dtype)
+        self.cam_k = CompatibleLinear(cam_dim, self.dim, bias=False, input_alignment=16).to(
+            device=device, dtype=dtype)
+        nn.init.zeros_(self.cam_q.weight)
+        nn.init.zeros_(self.cam_k.weight)
+
+    def _check_cam(self, qx, cam_tokens):
+        if cam_tokens is None:
+            return None
+        if self.cam_q is None or self.cam_k is None:
+            raise RuntimeError("camera_pose was provided but enable_camera_pose_qk() was not called")
+        if cam_tokens.shape[:2] != qx.shape[:2]:
+            raise ValueError(f"camera tokens shape {tuple(cam_tokens.shape[:2])} must match q/k "
+                             f"tokens {tuple(qx.shape[:2])}")
+        return cam_tokens.to(device=qx.device, dtype=qx.dtype)
+
+    def _apply_camera_qk(self, qx, kx, cam_tokens=None):
+        cam = self._check_cam(qx, cam_tokens)
+        if cam is None:
+            return qx, kx
+        cam = F.dropout(cam, p=self.cam_dropout_p, training=self.training)
+        return qx + self.cam_q(cam), kx + self.cam_k(cam)
+
+    # ---- projections ------------------------------------------------------------
+
+    def _project_self_attn_qkv(self, x, freqs, cam_tokens=None):
+        """Differentiable Q/K/V (attention.py:355-365)."""
+        qx, kx = self._apply_camera_qk(self.q(x), self.k(x), cam_tokens)
+        q = rope_apply(self.norm_q(qx), freqs, self.num_heads)
+        k = rope_apply(self.norm_k(kx), freqs, self.num_heads)
+        return q, k, self.v(x)
+
+    def _fused_ok(self, x, cam_tokens) -> bool:
+        dropout = cam_tokens is not None and self.training and self.cam_dropout_p > 0
+        return (x.is_cuda and x.dtype == torch.bfloat16 and x.shape[0] == 1 and not dropout and
+                self.q.weight.dtype == torch.bfloat16 and self.norm_q.weight.dtype == torch.bfloat16
+                and self.head_dim in (64, 128))
+
+    def _project_fused(self, x, freqs, cam_tokens=None):
+        """No-grad Q/K/V: GEMMs, then the fused HIP prologue.  Returns [S, H, D]."""
+        cam = self._check_cam(x, cam_tokens)
+        qx, kx, vx = (lin(x)[0].contiguous() for lin in (self.q, self.k, self.v))
+        cs, sn = freqs_to_cos_sin(freqs, device=x.device)
+        return qkv_prologue(
+            qx, kx, vx, norm_q_w=self.norm_q.weight, norm_k_w=self.norm_k.weight, rope_cos=cs,
+            rope_sin=sn, num_heads=self.num_heads, eps=self.norm_q.eps,
+            cam=None if cam is None else cam[0],
+            w_cam_q=None if cam is None else self.cam_q.weight,
+            w_cam_k=None if cam is None else self.cam_k.weight)
+
+    def _hier(self, x, freqs, tiles, cam_tokens, logits=None, geometry=None):
+        b, s, dim = x.shape
+        if b != 1:
+            raise NotImplementedError("hierarchical attention supports B=1")
+        H, D = self.num_heads, self.head_dim
+        if torch.is_grad_enabled():
+            q, k, v = self._project_self_attn_qkv(x, freqs, cam_tokens)
+            as4 = lambda t: t.to(torch.bfloat16).view(s, H, D)
+            y = hier_attention(as4(q), as4(k), as4(v), tiles, membership_logits=logits,
+                               ste_geometry=geometry)
+        else:
+            if self._fused_ok(x, cam_tokens):
+                q, k, v = self._project_fused(x, freqs, cam_tokens)
+            else:
+                q, k, v = (t.to(torch.bfloat16).view(s, H, D)
+                           for t in self._project_self_attn_qkv(x, freqs, cam_tokens))
+            y = torch.zeros((s, H, D), dtype=torch.bfloat16, device=x.device)
+            hier_attention_forward(q, k, v, tiles, y)
+        return self.o(y.reshape(1, s, dim).to(self.o.weight.dtype))
+
+    # ---- entry points -------------------------------------------------------------
+
+    def forward_hier_tiled_ste(self, x, freqs, mask, *, group_labels, active_group, num_players,
+                               num_frames, num_patches, num_groups, num_local_hub_tokens,
+                               num_global_hub_tokens, direct_player, tiled_layouts=None,
+                               cam_tokens=None):
+        """Full-sequence hierarchical attention (labels topology), reference
+        signature (attention.py:367-434)."""
+        if tiled_layouts is None:
+            tiled_layouts = M.build_hier_tiled_full_sequence_layouts(
+                device=x.device, num_players=num_players, num_frames=num_frames,
+                num_patches=num_patches, num_groups=num_groups,
+                num_local_hub_tokens=num_local_hub_tokens,
+                num_global_hub_tokens=num_global_hub_tokens,
+                num_frame_per_block=self.num_frame_per_block, local_attn_size=self.local_attn_size,
+                group_labels=group_labels, active_group=active_group, direct_player=direct_player)
+        tiles = tiled_layouts[0].tiles
+        if tiles is None or any(l.tiles is not tiles for l in tiled_layouts):
+            raise ValueError("tiled_layouts must come from one build_hier_tiled_full_sequence_layouts call")
+        return self._hier(x, freqs, tiles, cam_tokens)
+
+    def forward_hier_membership(self, x, freqs, *, num_players, num_frames, num_patches, num_groups,
+                                num_local_hub_tokens, num_global_hub_tokens, direct_player,
+                                membership=None, global_only=None, membership_logits=None,
+                                active_group=None, cam_tokens=None):
+        """Full-sequence hierarchical attention for a membership topology
+        ``[T, N, P]`` (hier_masks.py:127-193, 510-641).  With
+        ``membership_logits`` the hard membership is ``logits > 0`` and the
+        logits receive the straight-through gradient."""
+        P, T, L = int(num_players), int(num_frames), int(num_patches)
+        N, KL, KG = int(num_groups), int(num_local_hub_tokens), int(num_global_hub_tokens)
+        if membership_logits is not None:
+            if tuple(membership_logits.shape) != (T, N, P):
+                raise ValueError(f"membership_logits must be [T,N,P] = {(T, N, P)}")
+            mem = (membership_logits.detach() > 0).cpu().numpy()
+        elif membership is not None:
+            mem = torch.as_tensor(membership).detach().to("cpu", torch.bool).numpy().reshape(T, N, P)
+        else:
+            raise ValueError("membership or membership_logits is required")
+        go = (~mem.any(1) if global_only is None else
+              torch.as_tensor(global_only).detach().to("cpu", torch.bool).numpy().reshape(T, P))
+        act = None if active_group is None else \
+            torch.as_tensor(active_group).detach().to("cpu", torch.bool).numpy().reshape(T, N)
+        tiles = M.full_sequence_tiles(device=x.device, P=P, T=T, L=L, N=N, KL=KL, KG=KG,
+                                      n=self.num_frame_per_block, window=self.local_attn_size,
+                                      direct=direct_player, membership=mem, global_only=go,
+                                      active=act, no_local=self.hier_no_local_hub)
+        geometry = (P, T, L, N, KL) if membership_logits is not None else None
+        return self._hier(x, freqs, tiles, cam_tokens, logits=membership_logits, geometry=geometry)
+
+    def forward(self, x, freqs, mask=None, cam_tokens=None):
+        """attention.py:436-442 for dense boolean (or no) masks."""
+        if mask is not None and not torch.is_tensor(mask):
+            raise NotImplementedError(
+                "FlexAttention BlockMask masks are not available in this build; hierarchical "
+                "topologies use forward_hier_tiled_ste / forward_hier_membership")
+        q, k, v = self._project_self_attn_qkv(x, freqs, cam_tokens)
+        b, s, _ = q.shape
+        H = self.num_heads
+        split = lambda t: t.view(b, s, H, self.head_dim).transpose(1, 2)
+        am = None if mask is None else mask.to(device=q.device, dtype=torch.bool)
+        y = F.scaled_dot_product_attention(split(q), split(k), split(v), attn_mask=am)
+        return self.o(y.transpose(1, 2).reshape(b, s, self.dim))
