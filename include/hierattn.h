@@ -248,6 +248,31 @@ typedef struct HierBwdArgs {
 
 int hier_attn_bwd(const HierBwdArgs* args, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Paged KV cache append: copy the new K/V rows of a cached block into their */
+/* pool rows.  Replaces the per-stream rolling-cache writes and the per-call */
+/* pool concatenation of the cached path (attention.py:90-228, 605-666;     */
+/* hier_segmented_attention.py:458-469): every stream-frame owns a fixed    */
+/* page of pool rows, a re-run block overwrites its pages (refresh in place) */
+/* and a frame older than the window is overwritten by the newest one (the  */
+/* eviction), so no row ever moves.  Rows whose destination is outside      */
+/* [0, pool_rows) are skipped.                                              */
+/* ------------------------------------------------------------------------ */
+typedef struct HierPageArgs {
+  int32_t H, D;                    /* heads, head dim (multiple of 8)          */
+  int32_t n_rows;                  /* source rows                              */
+  int32_t pool_rows;               /* rows of each pool                        */
+  const uint16_t* k_src;           /* bf16 rows of the block                   */
+  const uint16_t* v_src;
+  int64_t k_src_ss, k_src_sh, v_src_ss, v_src_sh;
+  const int32_t* dst_rows;         /* [n_rows] DEVICE: pool row of each source row */
+  uint16_t* k_pool;                /* bf16 [pool_rows] rows                    */
+  uint16_t* v_pool;
+  int64_t pool_ss, pool_sh;        /* strides of both pools                    */
+} HierPageArgs;
+
+int hier_kv_append(const HierPageArgs* args, void* stream);
+
 /* Last error message of the calling thread ("" if none).                    */
 const char* hier_last_error(void);
 

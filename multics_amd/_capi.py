@@ -89,12 +89,21 @@ class HierBwdArgs(C.Structure):
                [("ste_stride_h", i64)]
 
 
+class HierPageArgs(C.Structure):
+    _fields_ = [("H", i32), ("D", i32), ("n_rows", i32), ("pool_rows", i32),
+                ("k_src", vp), ("v_src", vp)] + \
+               [(n, i64) for n in ("k_src_ss", "k_src_sh", "v_src_ss", "v_src_sh")] + \
+               [("dst_rows", vp), ("k_pool", vp), ("v_pool", vp), ("pool_ss", i64),
+                ("pool_sh", i64)]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],
+    "hier_kv_append": [C.POINTER(HierPageArgs), vp],
     "hier_last_error": [],
     "hier_version": [],
 }

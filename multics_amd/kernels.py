@@ -16,6 +16,7 @@ from typing import Optional, Sequence
 import torch
 
 from . import _capi
+from . import metadata as M
 from .metadata import HierTiledBlockLayout, TileList, ste_tiles, transpose_tiles
 
 
@@ -268,6 +269,99 @@ def hierarchical_tiled_full_sequence_attention(*, roped_q: torch.Tensor, roped_k
             for rng in tiles.item_ranges[b]:
                 hier_attention_forward(roped_q, roped_k, value, tiles, out, item_range=rng)
     return out.reshape(batch, seq_len, heads * head_dim)
+
+
+def _frame_list(frames: torch.Tensor, width: int) -> tuple:
+    """Frame id of each cached frame from a per-token frame tensor."""
+    if width <= 0:
+        return ()
+    return tuple(int(x) for x in frames.reshape(-1, width)[:, 0].tolist())
+
+
+def _active_frames(active_tokens: torch.Tensor, width: int) -> tuple:
+    if width <= 0:
+        return ()
+    return tuple(bool(x) for x in active_tokens.reshape(-1, width).any(dim=1).tolist())
+
+
+def hierarchical_cached_attention(*, roped_q, agent_frames, agent_keys, agent_vals, local_frames,
+                                  local_keys, local_vals, local_active_tokens, global_frames,
+                                  global_keys, global_vals, labels, active, P, N, L, KL, KG,
+                                  n_frames, n_block, local_attn, direct_player, membership=None,
+                                  global_only=None, hier_no_local_hub=False):
+    """The cached-backend plugin call (reference keyword set,
+    hier_segmented_attention.py:398-501, hier_tiled_attention.py:658-731,
+    hier_packed_attention.py:105-244, hier_paged_attention.py:79-268): per-stream
+    cache windows in, ``[1, S, H*D]`` out.  The streams are concatenated into
+    one K/V pool in the reference's pool order (as the reference backends do);
+    callers that keep their cache in a ``paged_cache.HierPagedKVCache`` skip
+    that copy (``SelfAttention.causal_forward``).  Labels and membership
+    topologies are both accepted."""
+    b, s, heads, head_dim = roped_q.shape
+    if b != 1 or head_dim not in (64, 128) or roped_q.dtype != torch.bfloat16:
+        raise NotImplementedError(
+            "hierarchical attention supports B=1, BF16, head_dim 64/128; "
+            f"got B={b}, dtype={roped_q.dtype}, head_dim={head_dim}")
+    if not roped_q.is_cuda:
+        raise NotImplementedError("hierarchical attention requires a GPU tensor")
+    no_local = bool(hier_no_local_hub)
+    agent_frame_lists = tuple(_frame_list(x, L) for x in agent_frames)
+    local_frame_lists = () if no_local else tuple(_frame_list(x, KL) for x in local_frames)
+    global_frame_list = _frame_list(global_frames, KG) if KG > 0 else ()
+    local_active_frames = () if no_local else tuple(_active_frames(x, KL)
+                                                    for x in local_active_tokens)
+    labels_cpu = None if labels is None else tuple(tuple(int(x) for x in r) for r in labels.tolist())
+    active_cpu = tuple(tuple(bool(x) for x in r) for r in active.tolist())
+    mem = None if membership is None else membership.detach().to("cpu", torch.bool).numpy()
+    go = None if global_only is None else global_only.detach().to("cpu", torch.bool).numpy()
+    tiles = M._build_metadata(
+        device=roped_q.device, P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n_frames, n_block=n_block,
+        local_attn=local_attn, agent_frame_lists=agent_frame_lists,
+        local_frame_lists=local_frame_lists, global_frame_list=global_frame_list,
+        local_active_frames=local_active_frames, labels=labels_cpu, q_active=active_cpu,
+        direct_player=bool(direct_player), block_m=16, membership=mem, global_only=go,
+        hier_no_local_hub=no_local, return_tiles=True)[6]
+    streams_k = list(agent_keys) + ([] if no_local else list(local_keys)) + [global_keys]
+    streams_v = list(agent_vals) + ([] if no_local else list(local_vals)) + [global_vals]
+    k = torch.cat(streams_k, dim=1).reshape(-1, heads, head_dim)
+    v = torch.cat(streams_v, dim=1).reshape(-1, heads, head_dim)
+    out = torch.zeros((s, heads, head_dim), dtype=torch.bfloat16, device=roped_q.device)
+    hier_attention_forward(roped_q[0], k, v, tiles, out)
+    return out.reshape(1, s, heads * head_dim)
+
+
+def hierarchical_segmented_attention(**kw):
+    """hier_segmented_attention.py:398-501 (labels topology)."""
+    if kw.get("membership") is not None:
+        raise ValueError("hierarchical_segmented_attention takes the labels topology; "
+                         "use hierarchical_paged_kv_attention for membership")
+    return hierarchical_cached_attention(**kw)
+
+
+def hierarchical_tiled_cached_attention(**kw):
+    """hier_tiled_attention.py:658-731 (labels topology)."""
+    if kw.get("membership") is not None:
+        raise ValueError("hierarchical_tiled_cached_attention takes the labels topology; "
+                         "use hierarchical_paged_kv_attention for membership")
+    return hierarchical_cached_attention(**kw)
+
+
+def hierarchical_packed_varlen_attention(**kw):
+    """hier_packed_attention.py:105-244."""
+    return hierarchical_cached_attention(**kw)
+
+
+def hierarchical_paged_kv_attention(**kw):
+    """hier_paged_attention.py:79-268 (inference only: refuses autograd inputs)."""
+    if any(torch.is_tensor(t) and t.requires_grad
+           for t in [kw.get("roped_q")] + list(kw.get("agent_keys", [])) + [kw.get("global_keys")]):
+        raise RuntimeError("hierarchical_paged_kv_attention is inference-only (inputs require grad)")
+    return hierarchical_cached_attention(**kw)
+
+
+def clear_hier_paged_state() -> None:
+    """hier_paged_attention.py:74-76: drop cached metadata."""
+    M.clear_metadata_cache()
 
 
 def qkv_prologue(qx: torch.Tensor, kx: torch.Tensor, vx: Optional[torch.Tensor], *,

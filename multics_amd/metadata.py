@@ -817,6 +817,33 @@ def full_sequence_tiles(*, device, P, T, L, N, KL, KG, n, window, direct, labels
     return hit
 
 
+def cached_tiles(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn, frames, tile_bases,
+                 local_active_frames, labels, q_active, direct_player, membership=None,
+                 global_only=None, hier_no_local_hub=False) -> TileList:
+    """Tile list of one cached call whose streams all hold the cached frames
+    ``frames`` (ascending, the current block's n frames last), with the K/V
+    rows of frame i of each stream at ``tile_bases`` = (agent [P][i], local
+    [N][i], global [i]) -- a paged pool.  Queries are the block in the cached
+    order [P*n*L | n*N*KL | n*KG].  Cached in the segmented-metadata LRU
+    (WAN_HIER_SEGMENTED_META_CACHE_SIZE), keyed by the topology and the pages."""
+    no_local = bool(hier_no_local_hub)
+    fr = tuple(int(x) for x in frames)
+    key = ("paged", str(torch.device(device)), P, N, L, KL, KG, n_frames, n_block, local_attn, fr,
+           _freeze(tile_bases), _freeze(local_active_frames), _freeze(labels), _freeze(q_active),
+           bool(direct_player), no_local, _freeze(membership), _freeze(global_only))
+    hit = _lru_get(_META_CACHE, key)
+    if hit is None:
+        topo = cached_topology(
+            P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n_frames, n_block=n_block, local_attn=local_attn,
+            agent_frame_lists=[fr] * P, local_frame_lists=[] if no_local else [fr] * N,
+            global_frame_list=fr if KG > 0 else (), local_active_frames=local_active_frames,
+            labels=labels, q_active=q_active, direct_player=direct_player, membership=membership,
+            global_only=global_only, hier_no_local_hub=no_local, tile_bases=tile_bases)
+        hit = build(topo, device).tiles
+        _lru_put(_META_CACHE, key, hit, "WAN_HIER_SEGMENTED_META_CACHE_SIZE", "64")
+    return hit
+
+
 def build_hier_tiled_cached_layout(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn,
                                    agent_frame_lists, local_frame_lists, global_frame_list,
                                    local_active_frames, labels, q_active, direct_player):

@@ -16,6 +16,10 @@ cam_q, cam_k``), mutable attributes and call signatures as the reference module
   straight-through gradient (``kernels.membership_grad``).
 * ``forward(x, freqs, mask=None, cam_tokens=None)`` -- dense boolean masks go
   to ``scaled_dot_product_attention`` as in the reference (attention.py:39-54).
+* ``causal_forward(...)`` / ``causal_forward_hier_hub(...)`` -- one block of a
+  chunked causal rollout through a ``paged_cache.HierPagedKVCache``
+  (attention.py:456-1043): the block's K/V go into their pool pages, the tile
+  list addresses the pool, one HIP forward computes every stream.
 
 Q/K/V projection: with autograd active, torch ops with the reference's
 rounding points (camera adapter, RMSNorm in fp32, RoPE in float64); without
@@ -33,7 +37,9 @@ import torch.nn.functional as F
 
 from . import metadata as M
 from .kernels import hier_attention, hier_attention_forward, qkv_prologue
+from .paged_cache import HierPagedKVCache
 from .rope import freqs_to_cos_sin
+from .topology import _prepare_hier_group_tensors, _prepare_hier_membership_tensors
 
 
 class RMSNorm(nn.Module):
@@ -162,6 +168,15 @@ class SelfAttention(nn.Module):
             w_cam_q=None if cam is None else self.cam_q.weight,
             w_cam_k=None if cam is None else self.cam_k.weight)
 
+    def _qkv_blocks(self, x, freqs, cam_tokens):
+        """[S, H, D] bf16 Q/K/V of a [1, S, dim] input (fused prologue when it applies)."""
+        s = x.shape[1]
+        H, D = self.num_heads, self.head_dim
+        if self._fused_ok(x, cam_tokens):
+            return self._project_fused(x, freqs, cam_tokens)
+        return tuple(t.to(torch.bfloat16).view(s, H, D)
+                     for t in self._project_self_attn_qkv(x, freqs, cam_tokens))
+
     def _hier(self, x, freqs, tiles, cam_tokens, logits=None, geometry=None):
         b, s, dim = x.shape
         if b != 1:
@@ -173,11 +188,7 @@ class SelfAttention(nn.Module):
             y = hier_attention(as4(q), as4(k), as4(v), tiles, membership_logits=logits,
                                ste_geometry=geometry)
         else:
-            if self._fused_ok(x, cam_tokens):
-                q, k, v = self._project_fused(x, freqs, cam_tokens)
-            else:
-                q, k, v = (t.to(torch.bfloat16).view(s, H, D)
-                           for t in self._project_self_attn_qkv(x, freqs, cam_tokens))
+            q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
             y = torch.zeros((s, H, D), dtype=torch.bfloat16, device=x.device)
             hier_attention_forward(q, k, v, tiles, y)
         return self.o(y.reshape(1, s, dim).to(self.o.weight.dtype))
@@ -245,3 +256,97 @@ class SelfAttention(nn.Module):
         am = None if mask is None else mask.to(device=q.device, dtype=torch.bool)
         y = F.scaled_dot_product_attention(split(q), split(k), split(v), attn_mask=am)
         return self.o(y.transpose(1, 2).reshape(b, s, self.dim))
+
+    # ---- cached rollout (attention.py:456-1043) ------------------------------------
+
+    def causal_forward_hier_hub(self, x, freqs, kv_cache, current_start=0, num_frames=None,
+                                num_players=None, num_hub_tokens=None, cam_tokens=None,
+                                group_labels=None, active_group=None, direct_player=False,
+                                membership=None, global_only=None):
+        """One block ``x [1, P*n*L + n*(N*KL+KG), dim]`` of a cached rollout.
+
+        Same checks and errors as the reference; the block's K/V are written
+        into ``kv_cache`` (refresh in place when the block is re-run) and the
+        block attends to the cached window of every stream."""
+        if not isinstance(kv_cache, HierPagedKVCache):
+            raise NotImplementedError("cached hierarchical attention runs on a "
+                                      "paged_cache.HierPagedKVCache")
+        b, s, dim = x.shape
+        if b != 1:
+            raise NotImplementedError("hierarchical attention supports B=1")
+        H, D = self.num_heads, self.head_dim
+        P = int(num_players if num_players is not None else kv_cache["num_players"])
+        N, KL, KG = int(kv_cache["num_groups"]), int(kv_cache["num_local_hub_tokens"]), \
+            int(kv_cache["num_global_hub_tokens"])
+        no_local = bool(getattr(self, "hier_no_local_hub", False))
+        if bool(kv_cache.get("hier_no_local_hub", False)) != no_local:
+            raise ValueError("hier_no_local_hub mismatch between SelfAttention and KV cache")
+        if P != kv_cache.P:
+            raise ValueError(f"num_players={P} does not match the KV cache ({kv_cache.P})")
+        n = int(num_frames)
+        k_total = int(num_hub_tokens if num_hub_tokens is not None else N * KL + KG)
+        if k_total != N * KL + KG:
+            raise ValueError(f"hier_hub K_total mismatch: {k_total} != {N}*{KL}+{KG}")
+        if no_local and (KL != 0 or KG <= 0):
+            raise ValueError("hier_no_local_hub cached attention requires K_L=0 and K_G>0; "
+                             f"got K_L={KL}, K_G={KG}")
+        use_mem = membership is not None
+        if use_mem:
+            mem, go, act = _prepare_hier_membership_tensors(membership, global_only, active_group,
+                                                            P, n, N, "cpu", allow_full_t=True)
+            labels = None
+        else:
+            labels, act = _prepare_hier_group_tensors(group_labels, active_group, P, n, N, "cpu")
+            if n > 1 and labels.numel() and not torch.equal(labels, labels[:1].expand_as(labels)):
+                raise ValueError("hier_hub cached inference requires group_labels constant inside "
+                                 "each latent block")
+        hub_len = n * k_total
+        agent_len = s - hub_len
+        if agent_len <= 0 or agent_len % (P * n) != 0:
+            raise ValueError(f"hier_hub causal seq shape invalid: S={s}, hub_len={hub_len}, P={P}, "
+                             f"n={n}")
+        L = agent_len // (P * n)
+        if L != kv_cache.L:
+            raise ValueError(f"tokens per player frame {L} do not match the KV cache ({kv_cache.L})")
+        if freqs.shape[0] != s:
+            raise ValueError("hier_hub causal_forward expects freqs.shape[0] == seq_len")
+        start_frame = int(current_start) // max(P * L, 1)
+        if use_mem:
+            T_full = int(mem.shape[0])
+            if start_frame < 0 or start_frame + n > T_full:
+                raise ValueError(f"hier_hub membership T={T_full} does not cover cached block "
+                                 f"[{start_frame},{start_frame + n})")
+            mb = mem[start_frame:start_frame + n]
+            gb = go[start_frame:start_frame + n]
+            if n > 1 and (not torch.equal(mb, mb[:1].expand_as(mb)) or
+                          not torch.equal(gb, gb[:1].expand_as(gb))):
+                raise ValueError("hier_hub cached inference requires membership / global_only "
+                                 "constant inside each latent block")
+            act = act[start_frame:start_frame + n]
+        q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
+        kv_cache.append(k, v, start_frame, n, act.numpy())
+        frames, bases, lact = kv_cache.window(start_frame + n - 1)
+        tiles = M.cached_tiles(
+            device=x.device, P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n,
+            n_block=int(self.num_frame_per_block), local_attn=int(self.local_attn_size),
+            frames=frames, tile_bases=bases, local_active_frames=lact,
+            labels=None if labels is None else labels.tolist(), q_active=act.tolist(),
+            direct_player=bool(direct_player),
+            membership=mem.numpy() if use_mem else None,
+            global_only=go.numpy() if use_mem else None, hier_no_local_hub=no_local)
+        out = torch.zeros((s, H, D), dtype=torch.bfloat16, device=x.device)
+        hier_attention_forward(q, kv_cache.k, kv_cache.v, tiles, out)
+        return self.o(out.reshape(1, s, dim).to(self.o.weight.dtype))
+
+    def causal_forward(self, x, freqs, mask=None, grid_sizes=None, seq_lens=None, kv_cache=None,
+                       current_start=0, cache_start=None, num_frames=None, num_players=None,
+                       num_hub_tokens=None, cam_tokens=None, group_labels=None, active_group=None,
+                       direct_player=False, membership=None, global_only=None):
+        """attention.py:1007-1043."""
+        if kv_cache is not None and kv_cache.get("hier_hub", False):
+            return self.causal_forward_hier_hub(
+                x, freqs, kv_cache, current_start=current_start, num_frames=num_frames,
+                num_players=num_players, num_hub_tokens=num_hub_tokens, cam_tokens=cam_tokens,
+                group_labels=group_labels, active_group=active_group, direct_player=direct_player,
+                membership=membership, global_only=global_only)
+        raise ValueError("Hierarchical causal attention requires a hier KV cache")

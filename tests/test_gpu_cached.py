@@ -1,0 +1,149 @@
+"""Cached rollout on the GPU: paged KV cache + HIP forward against the cached
+oracle (oracle/cached.py, pinned to the full-sequence mask), through the
+drop-in module and through the reference-named cached backend call."""
+
+import numpy as np
+import pytest
+import torch
+
+from multics_amd.kernels import hierarchical_paged_kv_attention, hierarchical_segmented_attention
+from multics_amd.module import SelfAttention
+from multics_amd.paged_cache import HierPagedKVCache
+from oracle.cached import HierCacheState, cached_block_forward
+from tests.gpu_util import err_stats, need_gpu, say
+
+pytestmark = pytest.mark.gpu
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def test_kv_append_scatters_rows():
+    need_gpu()
+    c = HierPagedKVCache(num_players=2, num_groups=2, num_patches=6, num_local_hub_tokens=2,
+                         num_global_hub_tokens=3, num_heads=3, head_dim=64, local_attn_size=2,
+                         num_frame_per_block=2, device="cuda")
+    S = 2 * 2 * 6 + 2 * (2 * 2 + 3)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    k = torch.randn(S, 3, 64, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(S, 3, 64, generator=g, device="cuda").to(torch.bfloat16)
+    say("kv append")
+    c.append(k, v, 5, 2, np.ones((2, 2), bool))
+    torch.cuda.synchronize()
+    rows = torch.from_numpy(c.block_rows(5, 2)).long().cuda()
+    assert torch.equal(c.k[rows], k) and torch.equal(c.v[rows], v)
+    other = torch.ones(c.k.shape[0], dtype=torch.bool, device="cuda")
+    other[rows] = False
+    assert torch.count_nonzero(c.k[other]) == 0
+
+
+def _module(dim, H, seed):
+    torch.manual_seed(seed)
+    m = SelfAttention(dim, H, eps=1e-6)
+    for lin in (m.q, m.k, m.v, m.o):
+        torch.nn.init.normal_(lin.weight, std=0.05)
+        torch.nn.init.zeros_(lin.bias)
+    return m.to("cuda", torch.bfloat16).eval()
+
+
+CASES = [
+    # name, P, T, L, N, KL, KG, n, W, H, D, direct, kind
+    ("labels_w3", 4, 9, 20, 2, 5, 6, 3, 3, 2, 128, True, "labels"),
+    ("labels_w6_nodirect", 3, 12, 16, 2, 2, 3, 3, 6, 2, 64, False, "labels"),
+    ("membership_w3", 4, 9, 12, 3, 2, 3, 3, 3, 2, 128, True, "membership"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_module_rollout_matches_cached_oracle(case):
+    need_gpu()
+    name, P, T, L, N, KL, KG, n, W, H, D, direct, kind = case
+    dim = H * D
+    m = _module(dim, H, seed=1)
+    m.num_frame_per_block, m.local_attn_size = n, W
+    rng = np.random.default_rng(2)
+    cache = HierPagedKVCache(num_players=P, num_groups=N, num_patches=L, num_local_hub_tokens=KL,
+                             num_global_hub_tokens=KG, num_heads=H, head_dim=D, local_attn_size=W,
+                             num_frame_per_block=n, device="cuda")
+    st = HierCacheState(P, N, L, KL, KG, H, D, W, n)
+    if kind == "membership":
+        mem = np.zeros((T, N, P), bool)
+        go = np.zeros((T, P), bool)
+        for b in range(T // n):
+            mb = rng.random((N, P)) < 0.45
+            mem[b * n:(b + 1) * n] = mb
+            go[b * n:(b + 1) * n] = ~mb.any(0) & (rng.random(P) < 0.7)
+    S = P * n * L + n * (N * KL + KG)
+    g = torch.Generator().manual_seed(3)
+    for b in range(T // n):
+        kw = dict(direct_player=direct)
+        okw = dict(n_block=n, direct=direct)
+        if kind == "membership":
+            kw.update(membership=torch.from_numpy(mem), global_only=torch.from_numpy(go))
+            okw.update(membership=mem, global_only=go)
+        else:
+            lab = np.repeat(rng.integers(0, N, size=(1, P)), n, axis=0)
+            act = np.zeros((n, N), bool)
+            act[np.arange(n)[:, None], lab] = True
+            kw.update(group_labels=torch.from_numpy(lab), active_group=torch.from_numpy(act))
+            okw.update(labels=lab, active=act)
+        ang = torch.rand(S, 1, D // 2, generator=g, dtype=torch.float64) * 6.283
+        freqs = torch.polar(torch.ones_like(ang), ang)
+        for step in range(2):       # two denoising passes over the block, then the next block
+            x = torch.randn(1, S, dim, generator=g).to("cuda", torch.bfloat16)
+            say(f"rollout {name} block {b} step {step}")
+            with torch.no_grad():
+                y = m.causal_forward(x, freqs, kv_cache=cache, current_start=b * n * P * L,
+                                     num_frames=n, num_players=P, **kw)
+                q, k, v = m._project_self_attn_qkv(x, freqs)
+            torch.cuda.synchronize()
+            as3 = lambda t: t[0].view(S, H, D).float().cpu()
+            att = cached_block_forward(st, as3(q), as3(k), as3(v), b * n, **okw)
+            ref = torch.nn.functional.linear(att.reshape(1, S, dim), m.o.weight.float().cpu(),
+                                             m.o.bias.float().cpu())
+            mx, mn = err_stats(y, ref)
+            say(f"  max-abs {mx:.3e} mean-abs {mn:.3e}")
+            assert mx <= MAX_ABS and mn <= MEAN_ABS
+
+
+def test_reference_cached_backend_call():
+    """The plugin keyword call on per-stream windows taken from the oracle's caches."""
+    need_gpu()
+    P, T, L, N, KL, KG, n, W, H, D = 3, 6, 16, 2, 2, 3, 3, 3, 2, 128
+    st = HierCacheState(P, N, L, KL, KG, H, D, W, n)
+    rng = np.random.default_rng(5)
+    g = torch.Generator().manual_seed(6)
+    S = P * n * L + n * (N * KL + KG)
+    for b in range(T // n):
+        lab = np.repeat(rng.integers(0, N, size=(1, P)), n, axis=0)
+        act = np.zeros((n, N), bool)
+        act[np.arange(n)[:, None], lab] = True
+        q, k, v = [(torch.randn(S, H, D, generator=g) * 0.5).to(torch.bfloat16).float()
+                   for _ in range(3)]
+        ref = cached_block_forward(st, q, k, v, b * n, n_block=n, direct=True, labels=lab,
+                                   active=act)
+        end = b * n + n - 1
+        frames = lambda c, w: (end - c.local_end // w + 1 + torch.arange(c.local_end) // w).cuda()
+        flat = lambda t: t.reshape(1, t.shape[0], H * D).to("cuda", torch.bfloat16)
+        kw = dict(
+            roped_q=q.to("cuda", torch.bfloat16)[None],
+            agent_frames=[frames(c, L) for c in st.agent],
+            agent_keys=[flat(c.k[:c.local_end]) for c in st.agent],
+            agent_vals=[flat(c.v[:c.local_end]) for c in st.agent],
+            local_frames=[frames(c, KL) for c in st.local],
+            local_keys=[flat(c.k[:c.local_end]) for c in st.local],
+            local_vals=[flat(c.v[:c.local_end]) for c in st.local],
+            local_active_tokens=[c.active[:c.local_end].cuda() for c in st.local],
+            global_frames=frames(st.glob, KG),
+            global_keys=flat(st.glob.k[:st.glob.local_end]),
+            global_vals=flat(st.glob.v[:st.glob.local_end]),
+            labels=torch.from_numpy(lab).cuda(), active=torch.from_numpy(act).cuda(),
+            P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=n, local_attn=W, direct_player=True)
+        say(f"plugin call block {b}")
+        for fn in (hierarchical_segmented_attention, hierarchical_paged_kv_attention):
+            y = fn(**kw)
+            torch.cuda.synchronize()
+            mx, mn = err_stats(y.reshape(S, H, D), ref)
+            say(f"  {fn.__name__}: max-abs {mx:.3e} mean-abs {mn:.3e}")
+            assert mx <= MAX_ABS and mn <= MEAN_ABS
+    with pytest.raises(RuntimeError):
+        kw["roped_q"] = kw["roped_q"].clone().requires_grad_(True)
+        hierarchical_paged_kv_attention(**kw)
