@@ -9,8 +9,13 @@ launch, Q/K/V already resident in HBM.  Metadata (topology build) is built
 once before timing, like the reference's cached layouts; its device latency is
 reported separately, as is the fused Q/K prologue.
 
-Prints one JSON line (the driver contract).  ``--config c3|c4|...`` runs the
-other player counts for the DESIGN tables instead.
+Prints one JSON line (the driver contract).  ``--config p6|c3|p10|...`` makes
+another full-sequence configuration the headline line.  Unless ``--no-suite``,
+the line's ``extra.suite`` also carries, from the same run: the forward at 6, 8
+and 10 players; the training step of BASELINE config C5 (forward + backward +
+membership STE, P=4, T=21, W=7); and the per-chunk latency of the cached
+rollout of config C4 (10 players, chunks of 6 frames through the paged KV
+cache, steady state of the denoising passes).
 """
 
 from __future__ import annotations
@@ -40,6 +45,8 @@ CONFIGS = {
     "p6": (6, 42, 220, 3, 5, 6, 3, 21, 24, 128, "pairs"),
     "c3": (8, 42, 220, 3, 5, 6, 3, 21, 24, 128, "dynamic"),
     "p10": (10, 42, 220, 4, 5, 6, 3, 21, 24, 128, "random_block"),
+    "c5": (4, 21, 220, 2, 5, 6, 3, 7, 24, 128, "logits"),
+    "c4": (10, 42, 220, 4, 5, 6, 3, 21, 24, 128, "random_block"),
 }
 
 
@@ -80,6 +87,12 @@ def grouping(name, P, T, N, rng):
                 mem[t, slot, g] = True
             go[t] = ~mem[t].any(0)
         return None, mem, go
+    if name == "logits":
+        # soft membership logits ~ N(0,1) per (frame, group, player), constant
+        # inside each 3-frame block; the hard membership is logits > 0
+        lg = np.repeat(rng.standard_normal((T // 3, N, P)), 3, axis=0)[:T]
+        mem = lg > 0
+        return lg, mem, ~mem.any(1)
     if name == "random_block":
         mem = np.zeros((T, N, P), dtype=bool)
         for b in range(0, T, 3):
@@ -96,14 +109,15 @@ def build_case(cfg, device):
     from multics_amd import metadata as M
     P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS[cfg]
     rng = np.random.default_rng(SEED)
-    labels, mem, go = grouping(grp, P, T, N, rng)
+    first, mem, go = grouping(grp, P, T, N, rng)
+    labels = None if grp == "logits" else first      # "logits": first = the soft logits
     topo = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W, direct=True,
                                     labels=labels, membership=mem, global_only=go)
     t0 = time.perf_counter()
     res = M.build(topo, device)
     torch.cuda.synchronize()
     host_build_s = time.perf_counter() - t0
-    return topo, res.tiles, host_build_s, (labels, mem, go)
+    return topo, res.tiles, host_build_s, (first, mem, go)
 
 
 def time_events(fn, steps, warmup):
@@ -160,6 +174,116 @@ def cpu_baseline(cfg, topo_args, budget_s=20.0):
                 cpu=platform.processor() or platform.machine())
 
 
+def bench_forward_cfg(cfg, dev, steps=10, warmup=3):
+    """Full-sequence forward of another configuration: ms and useful TFLOP/s."""
+    from multics_amd.kernels import hier_attention_forward
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS[cfg]
+    topo, tiles, _, _ = build_case(cfg, dev)
+    S = P * T * L + T * (N * KL + KG)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    q, k, v = ((torch.randn(H, S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+               .permute(1, 0, 2) for _ in range(3))
+    out = torch.empty(S, H, D, dtype=torch.bfloat16, device=dev)
+    ms = float(np.median(time_events(lambda: hier_attention_forward(q, k, v, tiles, out),
+                                     steps, warmup)))
+    flop = 4.0 * H * D * tiles.logical_pairs
+    del q, k, v, out
+    return {"players": P, "tokens": S, "ms_per_layer": round(ms, 4),
+            "useful_tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+            "frac_peak": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "grouping": grp}
+
+
+def bench_training(dev, steps=10, warmup=3):
+    """Config C5: forward + backward + membership STE of one attention layer."""
+    from multics_amd.kernels import hier_attention
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS["c5"]
+    topo, tiles, _, (logits, mem, go) = build_case("c5", dev)
+    S = P * T * L + T * (N * KL + KG)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    mk = lambda: (torch.randn(H, S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16) \
+        .permute(1, 0, 2).contiguous().requires_grad_(True)
+    q, k, v = mk(), mk(), mk()
+    dout = torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16)
+    lg = torch.from_numpy(logits).float().to(dev).requires_grad_(True)
+    geo = (P, T, L, N, KL)
+
+    def fwd():
+        return hier_attention(q, k, v, tiles, membership_logits=lg, ste_geometry=geo)
+
+    def step():
+        q.grad = k.grad = v.grad = lg.grad = None
+        fwd().backward(dout)
+
+    ms_fwd = float(np.median(time_events(lambda: fwd(), steps, warmup)))
+    ms_step = float(np.median(time_events(step, steps, warmup)))
+    E = tiles.logical_pairs
+    flop_f, flop_b = 4.0 * H * D * E, 10.0 * H * D * E
+    ms_bwd = ms_step - ms_fwd
+    return {"players": P, "frames": T, "window": W, "tokens": S, "useful_pairs": E,
+            "ms_fwd": round(ms_fwd, 4), "ms_fwd_bwd": round(ms_step, 4),
+            "ms_bwd": round(ms_bwd, 4),
+            "useful_tflops_fwd_bwd": round((flop_f + flop_b) / (ms_step * 1e-3) / 1e12, 2),
+            "useful_tflops_bwd": round(flop_b / (ms_bwd * 1e-3) / 1e12, 2),
+            "note": "bwd = dQ (query-major) + dK/dV (key-major) + membership STE pass; "
+                    "useful FLOP 4*H*D*E fwd, 10*H*D*E bwd"}
+
+
+def bench_rollout(dev, passes=10):
+    """Config C4: cached rollout, 10 players, chunk = 6 latent frames = 2 blocks
+    of 3 through the paged KV cache; time one denoising pass over a chunk in
+    the steady state (window full, metadata cached)."""
+    from multics_amd import metadata as M
+    from multics_amd.kernels import hier_attention_forward
+    from multics_amd.paged_cache import HierPagedKVCache
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS["c4"]
+    rng = np.random.default_rng(SEED)
+    _, mem, go = grouping(grp, P, T, N, rng)
+    act_full = mem.any(-1)
+    cache = HierPagedKVCache(num_players=P, num_groups=N, num_patches=L, num_local_hub_tokens=KL,
+                             num_global_hub_tokens=KG, num_heads=H, head_dim=D, local_attn_size=W,
+                             num_frame_per_block=n, device=dev)
+    S = P * n * L + n * (N * KL + KG)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    q, k, v = ((torch.randn(S, H, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+               for _ in range(3))
+    out = torch.empty(S, H, D, dtype=torch.bfloat16, device=dev)
+
+    def block_tiles(b):
+        frames, bases, lact = cache.window(b * n + n - 1)
+        return M.cached_tiles(device=dev, P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=n,
+                              local_attn=W, frames=frames, tile_bases=bases,
+                              local_active_frames=lact, labels=None,
+                              q_active=act_full[b * n:b * n + n].tolist(), direct_player=True,
+                              membership=mem, global_only=go)
+
+    first = (W + n) // n                     # blocks that fill the window
+    for b in range(first):
+        cache.append(k, v, b * n, n, act_full[b * n:b * n + n])
+    chunk = [first, first + 1]
+    t0 = time.perf_counter()
+    tl = {}
+    for b in chunk:
+        cache.append(k, v, b * n, n, act_full[b * n:b * n + n])
+        tl[b] = block_tiles(b)
+    torch.cuda.synchronize()
+    meta_ms = (time.perf_counter() - t0) * 1e3 / len(chunk)
+
+    def one_pass():
+        for b in chunk:
+            cache.append(k, v, b * n, n, act_full[b * n:b * n + n])
+            hier_attention_forward(q, cache.k, cache.v, tl[b], out)
+
+    ms = float(np.median(time_events(one_pass, passes, 3)))
+    pairs = sum(tl[b].logical_pairs for b in chunk)
+    return {"players": P, "chunk_frames": 2 * n, "query_rows": 2 * S,
+            "cached_frames_per_stream": cache.R, "ms_per_chunk": round(ms, 4),
+            "useful_tflops": round(4.0 * H * D * pairs / (ms * 1e-3) / 1e12, 2),
+            "first_pass_metadata_ms_per_block": round(meta_ms, 2),
+            "note": "per denoising pass: paged append + HIP forward for 2 blocks; metadata "
+                    "is built on a block's first pass and reused by its later passes"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +292,8 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--no-suite", action="store_true",
+                    help="skip the other configurations (6/8/10 players, training, rollout)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -268,6 +394,14 @@ def main():
         "extra": {"metadata_build_ms": round(float(np.median(meta_ms)), 3),
                   "prologue_ms": round(pro_ms, 4), "work_items": tiles.n_items * H},
     }
+    if not args.no_suite:
+        suite = {}
+        for cfg in ("p6", "c3", "p10"):
+            if cfg != args.config:
+                suite[f"fwd_{cfg}"] = bench_forward_cfg(cfg, dev)
+        suite["training_c5"] = bench_training(dev)
+        suite["rollout_c4"] = bench_rollout(dev)
+        line["extra"]["suite"] = suite
     print(json.dumps(line), flush=True)
 
 
