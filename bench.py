@@ -120,6 +120,17 @@ def build_case(cfg, device):
     return topo, res.tiles, host_build_s, (first, mem, go)
 
 
+def profiled_traffic(cfg):
+    """HBM bytes per launch of the forward kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of the same workload (counter values scaled
+    by the copy-kernel calibration recorded with them), or None."""
+    f = ROOT / "profiles" / f"attn_fwd_{cfg}.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    return int(d["traffic_bytes_per_launch"])
+
+
 def time_events(fn, steps, warmup):
     for _ in range(warmup):
         fn()
@@ -389,7 +400,7 @@ def main():
                    "useful_gflop": round(useful_flop / 1e9, 1), "seed": SEED},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": profiled_traffic(args.config)},
         "cpu_baseline": cpu,
         "extra": {"metadata_build_ms": round(float(np.median(meta_ms)), 3),
                   "prologue_ms": round(pro_ms, 4), "work_items": tiles.n_items * H},
