@@ -14,9 +14,13 @@ cites the reference file:line it follows.  Modules:
 * ``masks``      -- the dense hierarchical mask rule, labels / membership /
                     no-local forms (``multics/models/hier_masks.py:364-641``).
 * ``attention``  -- masked SDPA in fp32, RMSNorm, camera Q/K adapter, RoPE
-                    and freqs builders, camera12, rolling KV cache and the
-                    cached per-stream forward (``multics/models/attention.py``,
+                    and freqs builders, camera12 (``multics/models/attention.py``,
                     ``multics/models/rope.py``, ``multics/data/*.py``).
+* ``cached``     -- the rolling per-stream KV cache and the cached per-stream
+                    forward of a rollout block (``multics/models/attention.py:
+                    90-228, 456-1005``).
+* ``ste``        -- the fp32 autograd definition of the membership
+                    straight-through gradient (no reference counterpart).
 
 Parity pins (what each function is checked against) are listed in the module
 headers; a function with no independent check says "parity unpinned".
