@@ -19,6 +19,8 @@ STRUCTS = {
     "HierMetaOut": _capi.HierMetaOut,
     "HierPrologueArgs": _capi.HierPrologueArgs,
     "HierFwdArgs": _capi.HierFwdArgs,
+    "HierBwdArgs": _capi.HierBwdArgs,
+    "HierPageArgs": _capi.HierPageArgs,
 }
 
 
