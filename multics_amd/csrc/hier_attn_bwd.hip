@@ -564,6 +564,10 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
                    span_bytes(a.q_rows, a.q_ss, a.q_sh, a.H, a.D) <= (1ll << 32) &&
                    span_bytes(a.q_rows, a.do_ss, a.do_sh, a.H, a.D) <= (1ll << 32),
                HIER_EUNSUPPORTED, "Q/K/V/dO views must span at most 4 GiB");
+  HIER_REQUIRE(copy_rows_ok(a.kv_rows, a.k_ss) && copy_rows_ok(a.kv_rows, a.v_ss) &&
+                   copy_rows_ok(a.q_rows, a.q_ss) && copy_rows_ok(a.q_rows, a.do_ss),
+               HIER_EUNSUPPORTED,
+               "Q/K/V/dO need at most 2^24 rows and a row stride under 8M elements");
   HIER_REQUIRE(a.n_ste_items >= 0, HIER_EINVAL, "n_ste_items must be >= 0");
   if (a.n_ste_items > 0) {
     HIER_REQUIRE(a.ste_items && a.ste_kv_idx && a.ste_kv_mask && a.ste_kv_class && a.ste_partial &&

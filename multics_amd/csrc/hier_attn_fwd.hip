@@ -46,14 +46,15 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kRescaleLog2 = 8.0f;   // lazy-rescale threshold (exp2 units)
 
-// LDS of a workgroup: K[2] | V[2] | masks[2] (one dword per key).  K tiles are
-// only read as rows, V tiles only transposed.
-template <int D>
-struct Lds {
-  static constexpr int KOFF = 0;
-  static constexpr int VOFF = 2 * Geo<D>::TILEB;
-  static constexpr int MOFF = 4 * Geo<D>::TILEB;
-  static constexpr int SIZE = 4 * Geo<D>::TILEB + 2 * Geo<D>::MBYTES;
+// LDS stages of a workgroup: K[2], V[2], masks[2] (one dword per key), each
+// its own __shared__ array.  K tiles are only read as rows, V tiles only
+// transposed.  Distinct arrays let the compiler see that the copies into one
+// stage never alias the reads of the other; given one array it waits for every
+// outstanding copy before the first LDS read that follows them.
+struct Stages {
+  char* k[2];
+  char* v[2];
+  char* m[2];
 };
 
 // ---- per-sub-block state and math ------------------------------------------
@@ -233,24 +234,22 @@ struct Ctx {
 
 // Half-step j = 2t + B of the pipeline: QK of block B of tile t+1 into sq,
 // softmax of block j+1 (sc: block 1 of tile t for B = 0, block 0 of tile t+1
-// for B = 1) into pn, PV of block B of tile t with pv; then the masks of sq.
-// The three streams are independent, so one scheduling region interleaves
-// them: each MFMA is followed by a few softmax VALU instructions and the LDS
-// reads of the MFMAs two or three slots ahead.  PAR = t & 1 selects the LDS
-// stages: K(t+1) and its masks in PAR^1, V(t) in PAR.
+// for B = 1) into pn, PV of block B of tile t with pv; then the masks of sq
+// (blk_cur: visibility flags of tile t+1).  The three streams are independent,
+// so one scheduling region interleaves them: each MFMA is followed by a few
+// softmax VALU instructions and the LDS reads of the MFMAs two or three slots
+// ahead.  PAR = t & 1 selects the LDS stages: K(t+1) and its masks in PAR^1,
+// V(t) in PAR.
 template <int D, int PAR, int B>
 __device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& sq,
                                           const f32x16& sc, const bf16x8* pv, bf16x8* pn,
-                                          bool& resc, float& alpha_pend, char* lds) {
-  constexpr int TB = Geo<D>::TILEB;
+                                          bool& resc, float& alpha_pend, uint32_t blk_cur,
+                                          const Stages& st) {
   if (resc) rescale<D>(R, alpha_pend);
-  sq = qk_block<D>(R.q, lds + Lds<D>::KOFF + (PAR ^ 1) * TB, c.ra, B);
+  sq = qk_block<D>(R.q, st.k[PAR ^ 1], c.ra, B);
   resc = softmax_block<D>(R, sc, pn, c.c2, c.thr);
   alpha_pend = R.alpha;
-  // keep the softmax results in this region (otherwise they sink into later
-  // blocks, away from the MFMAs they are meant to overlap)
-  asm volatile("" : "+v"(pn[0]), "+v"(pn[1]), "+v"(R.l), "+v"(alpha_pend));
-  pv_block<D>(R, pv, lds + Lds<D>::VOFF + PAR * TB, c.ra, B);
+  pv_block<D>(R, pv, st.v[PAR], c.ra, B);
   // NC + 2*NDB MFMAs and NC + 4*NDB LDS reads: three reads per two MFMAs
   constexpr int NM = Geo<D>::NC + 2 * Geo<D>::NDB;
   __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
@@ -263,33 +262,41 @@ __device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
   }
-  if ((c.blk[t + 1] & R.bits) != R.bits)
-    mask_block(sq, lds + Lds<D>::MOFF + (PAR ^ 1) * Geo<D>::MBYTES, B, R.qframe, c.lane);
+  // keep the softmax results in this region (otherwise they sink past the
+  // mask branch, away from the MFMAs they are meant to overlap)
+  asm volatile("" : "+v"(pn[0]), "+v"(pn[1]), "+v"(R.l), "+v"(alpha_pend));
+  if ((blk_cur & R.bits) != R.bits)
+    mask_block(sq, st.m[PAR ^ 1], B, R.qframe, c.lane);
 }
 
 // Tile iteration t (t + 1 < nt): copies K(t+2) + masks into stage PAR and
-// V(t+1) into stage PAR^1, runs half-steps 2t and 2t+1.  Invariant on entry:
-// K(t+1), masks(t+1) and V(t) resident; S(2t+1) (sb) masked; P(2t) (pa)
-// ready with its rescale pending.
+// V(t+1) into stage PAR^1, loads the key indices and visibility flags of the
+// next iteration, runs half-steps 2t and 2t+1.  Invariant on entry: K(t+1),
+// masks(t+1) and V(t) resident; S(2t+1) (sb) masked; P(2t) (pa) ready with its
+// rescale pending; ik / iv / blk hold the indices of tiles min(t+2, nt-1) /
+// t+1 and the flags of tile t+1.  Every global load of the iteration is waited
+// for with the copies at its end, so nothing inside the half-steps waits on
+// the copies in flight.
 template <int D, int PAR>
 __device__ __forceinline__ void tile_iter(Ctx<D>& c, Rows<D>& R, int t, f32x16& sa, f32x16& sb,
                                           bf16x8* pa, bf16x8* pb, bool& resc, float& alpha_pend,
-                                          Idx<D>& ik, Idx<D>& iv, char* lds) {
-  constexpr int TB = Geo<D>::TILEB;
+                                          Idx<D>& ik, Idx<D>& iv, uint32_t& blk, const Stages& st) {
   if (t + 2 < c.nt) {
-    copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, ik, lds + Lds<D>::KOFF + PAR * TB, c.wave);
+    copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, ik, st.k[PAR], c.wave);
     if (c.wave == 0)
-      copy_dwords(c.kv_mask + (t + 2) * kSlab, lds + Lds<D>::MOFF + PAR * Geo<D>::MBYTES, c.lane);
+      copy_dwords(c.kv_mask + (t + 2) * kSlab, st.m[PAR], c.lane);
   }
-  copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, iv, lds + Lds<D>::VOFF + (PAR ^ 1) * TB, c.wave);
+  copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, iv, st.v[PAR ^ 1], c.wave);
   ik = load_idx<D>(c.kv_idx, min(t + 3, c.nt - 1), c.ck.idx_off);
   iv = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+  const uint32_t blk_pre = c.blk[min(t + 2, c.nt - 1)];
   if (c.active) {
-    half_step<D, PAR, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, lds);
-    half_step<D, PAR, 1>(c, R, t, sb, sa, pb, pa, resc, alpha_pend, lds);
+    half_step<D, PAR, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, blk, st);
+    half_step<D, PAR, 1>(c, R, t, sb, sa, pb, pa, resc, alpha_pend, blk, st);
   }
   wait_copies();
   __syncthreads();
+  blk = blk_pre;
 }
 
 // Last tile (t = nt - 1): softmax of its block 1 (sb) into pb, PV of both
@@ -297,8 +304,8 @@ __device__ __forceinline__ void tile_iter(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
 template <int D, int PAR>
 __device__ __forceinline__ void tail(Ctx<D>& c, Rows<D>& R, const HierFwdArgs& a, int head,
                                      const f32x16& sb, const bf16x8* pa, bf16x8* pb, bool resc,
-                                     float alpha_pend, char* lds) {
-  const char* vs = lds + Lds<D>::VOFF + PAR * Geo<D>::TILEB;
+                                     float alpha_pend, const Stages& st) {
+  const char* vs = st.v[PAR];
   if (resc) rescale<D>(R, alpha_pend);
   resc = softmax_block<D>(R, sb, pb, c.c2, c.thr);
   alpha_pend = R.alpha;
@@ -310,7 +317,10 @@ __device__ __forceinline__ void tail(Ctx<D>& c, Rows<D>& R, const HierFwdArgs& a
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, int total) {
-  __shared__ __align__(16) char lds[Lds<D>::SIZE];
+  __shared__ __align__(16) char lds_k0[Geo<D>::TILEB], lds_k1[Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_v0[Geo<D>::TILEB], lds_v1[Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_m0[Geo<D>::MBYTES], lds_m1[Geo<D>::MBYTES];
+  const Stages st = {{lds_k0, lds_k1}, {lds_v0, lds_v1}, {lds_m0, lds_m1}};
   // XCD-aware mapping: consecutive logical items land on the same XCD (the
   // dispatcher round-robins workgroups over 8 XCDs), so items sharing a head
   // and overlapping key windows share one L2.
@@ -349,13 +359,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
     if (c.active) store_rows<D>(R, a, head, c.lane, 0.f, -INFINITY);
     return;
   }
-  constexpr int TB = Geo<D>::TILEB;
-  char* const kst0 = lds + Lds<D>::KOFF;
-  char* const vst0 = lds + Lds<D>::VOFF;
-  char* const mst0 = lds + Lds<D>::MOFF;
+  char* const kst0 = st.k[0];
+  char* const vst0 = st.v[0];
+  char* const mst0 = st.m[0];
 
   // prologue: K(0), V(0), K(1) and masks(0, 1) resident; S(0), S(1) (both
-  // blocks of tile 0) computed and masked; P(0) from the softmax of S(0).
+  // blocks of tile 0) computed and masked; P(0) from the softmax of S(0); the
+  // first iteration's indices and flags loaded before the wait.
+  Idx<D> ik, iv;
+  uint32_t blk;
   {
     const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
     copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i0, kst0, c.wave);
@@ -363,14 +375,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
     if (c.wave == 0) copy_dwords(c.kv_mask, mst0, c.lane);
     if (nt > 1) {
       const Idx<D> i1 = load_idx<D>(c.kv_idx, 1, c.ck.idx_off);
-      copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i1, kst0 + TB, c.wave);
-      if (c.wave == 0) copy_dwords(c.kv_mask + kSlab, mst0 + Geo<D>::MBYTES, c.lane);
+      copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i1, st.k[1], c.wave);
+      if (c.wave == 0) copy_dwords(c.kv_mask + kSlab, st.m[1], c.lane);
     }
+    ik = load_idx<D>(c.kv_idx, min(2, nt - 1), c.ck.idx_off);
+    iv = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
+    blk = c.blk[min(1, nt - 1)];
     wait_copies();
     __syncthreads();
   }
-  Idx<D> ik = load_idx<D>(c.kv_idx, min(2, nt - 1), c.ck.idx_off);
-  Idx<D> iv = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
   f32x16 sa, sb;
   bf16x8 pa[2], pb[2];
   bool resc = false;
@@ -391,14 +404,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
   // is a compile-time constant
   int t = 0;
   for (; t + 2 < nt; t += 2) {
-    tile_iter<D, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, ik, iv, lds);
-    tile_iter<D, 1>(c, R, t + 1, sa, sb, pa, pb, resc, alpha_pend, ik, iv, lds);
+    tile_iter<D, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, ik, iv, blk, st);
+    tile_iter<D, 1>(c, R, t + 1, sa, sb, pa, pb, resc, alpha_pend, ik, iv, blk, st);
   }
   if (t + 1 < nt) {
-    tile_iter<D, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, ik, iv, lds);
-    if (c.active) tail<D, 1>(c, R, a, head, sb, pa, pb, resc, alpha_pend, lds);
+    tile_iter<D, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, ik, iv, blk, st);
+    if (c.active) tail<D, 1>(c, R, a, head, sb, pa, pb, resc, alpha_pend, st);
   } else {
-    if (c.active) tail<D, 0>(c, R, a, head, sb, pa, pb, resc, alpha_pend, lds);
+    if (c.active) tail<D, 0>(c, R, a, head, sb, pa, pb, resc, alpha_pend, st);
   }
 }
 
@@ -429,6 +442,8 @@ extern "C" int hier_attn_fwd(const HierFwdArgs* args, void* stream) {
   HIER_REQUIRE(k_ext <= (1ll << 32) && v_ext <= (1ll << 32), HIER_EUNSUPPORTED,
                "K/V views must span at most 4 GiB (got %lld / %lld bytes)", (long long)k_ext,
                (long long)v_ext);
+  HIER_REQUIRE(copy_rows_ok(a.kv_rows, a.k_ss) && copy_rows_ok(a.kv_rows, a.v_ss),
+               HIER_EUNSUPPORTED, "K/V need at most 2^24 rows and a row stride under 8M elements");
   if (a.n_items == 0) return HIER_OK;
   const int64_t total = (int64_t)a.n_items * a.H;
   HIER_REQUIRE(total < (1ll << 31) - 8, HIER_EUNSUPPORTED, "too many work items");

@@ -122,13 +122,20 @@ __device__ __forceinline__ Idx<D> load_idx(const int32_t* idx, int tile, int idx
   return r;
 }
 
+// The copies address a row as row * row_stride_bytes with one 24 x 24-bit
+// multiply: the entry points check this bound on the views they copy from
+// (their 4 GiB span bound then keeps the product within 32 bits).
+__host__ __device__ constexpr bool copy_rows_ok(int64_t rows, int64_t row_stride_elems) {
+  return rows <= (1ll << 24) && row_stride_elems * 2 < (1ll << 24);
+}
+
 // Copy e of one tile: 16 bytes per lane, 1 KB per wave instruction.  g points
 // at the head's first element of row 0 of the source tensor; rows are
 // addressed with 32-bit byte offsets.
 template <int D, int S>
 __device__ __forceinline__ void copy_one(const char* g, uint32_t ss_bytes, const Copier<D, S>& cp,
                                          const Idx<D>& ix, int e, char* slot, int wave) {
-  uint32_t off = (uint32_t)ix.v[e] * ss_bytes + cp.add(e);
+  uint32_t off = __umul24((uint32_t)ix.v[e], ss_bytes) + cp.add(e);
   // opaque 32-bit offset: the copy then uses the scalar-base + 32-bit
   // vector-offset address form instead of a 64-bit per-lane address
   asm volatile("" : "+v"(off));

@@ -81,3 +81,19 @@ def test_null_arguments_are_rejected_without_a_gpu():
     assert lib.hier_qkv_prologue(None, None) == _capi.HIER_EINVAL
     assert lib.hier_meta_count(None, None, None) == _capi.HIER_EINVAL
     assert lib.hier_meta_build(None, None, None) == _capi.HIER_EINVAL
+
+
+def test_forward_rejects_views_past_the_24_bit_row_limit_without_a_gpu():
+    """The tile copies address rows with a 24 x 24-bit multiply: more than 2^24
+    K/V rows is refused before anything is launched (n_items = 0 here, so no
+    kernel could run even if the check were missing)."""
+    lib = _capi.lib()
+    fake = 1 << 20   # 16-byte aligned, never dereferenced
+    a = _capi.HierFwdArgs(H=1, D=64, n_items=0, scale=0.125, kv_rows=(1 << 24) + 1,
+                          q=fake, k=fake, v=fake, o=fake, q_ss=64, q_sh=64, k_ss=64, k_sh=64,
+                          v_ss=64, v_sh=64, o_ss=64, o_sh=64, tile_items=fake, tile_kv_idx=fake,
+                          tile_kv_mask=fake, tile_blk_and=fake)
+    assert lib.hier_attn_fwd(C.byref(a), None) == _capi.HIER_EUNSUPPORTED
+    assert b"2^24" in lib.hier_last_error()
+    a.kv_rows = 1 << 24
+    assert lib.hier_attn_fwd(C.byref(a), None) == _capi.HIER_OK
