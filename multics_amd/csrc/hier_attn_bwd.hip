@@ -91,13 +91,14 @@ __device__ __forceinline__ uint32_t keep_mask(uint32_t bits, int bit) {
 
 // ---- dQ (query-major) --------------------------------------------------------
 
-// LDS: K[2] (rows and transposed) | V[2] (rows) | masks[2]
-template <int D>
-struct QLds {
-  static constexpr int KOFF = 0;
-  static constexpr int VOFF = 2 * Geo<D>::TILEB;
-  static constexpr int MOFF = 4 * Geo<D>::TILEB;
-  static constexpr int SIZE = 4 * Geo<D>::TILEB + 2 * Geo<D>::MBYTES;
+// LDS stages: K[2] (rows and transposed) | V[2] (rows) | masks[2], each its
+// own __shared__ array.  Distinct arrays let the compiler see that the copies
+// into one stage never alias the reads of the other; given one array it waits
+// for every outstanding copy before the first LDS read that follows them.
+struct QStages {
+  char* k[2];
+  char* v[2];
+  char* m[2];
 };
 
 template <int D>
@@ -124,20 +125,26 @@ struct QCtx {
   uint32_t bits;
 };
 
+// Tile t: copies tile t+1 into stage PAR^1 and loads the key indices and the
+// visibility flags of tile t+1 (blk: flags of tile t on entry, of t+1 on
+// exit), then works on stage PAR.  Every global load is waited for with the
+// copies at the end, so nothing in the MFMA work waits on the copies in flight.
 template <int D, int PAR>
-__device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, char* lds) {
-  constexpr int TB = Geo<D>::TILEB;
+__device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, uint32_t& blk,
+                                        const QStages& st) {
+  uint32_t blk_next = 0;
   if (t + 1 < c.nt) {
-    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, lds + QLds<D>::KOFF + (PAR ^ 1) * TB, c.wave);
-    copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, inext, lds + QLds<D>::VOFF + (PAR ^ 1) * TB, c.wave);
-    copy_dwords(c.kv_mask + (t + 1) * kSlab, lds + QLds<D>::MOFF + (PAR ^ 1) * Geo<D>::MBYTES, c.lane);
+    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, st.k[PAR ^ 1], c.wave);
+    copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, inext, st.v[PAR ^ 1], c.wave);
+    copy_dwords(c.kv_mask + (t + 1) * kSlab, st.m[PAR ^ 1], c.lane);
     inext = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+    blk_next = c.blk[t + 1];
   }
   if (c.active) {
-    const char* ks = lds + QLds<D>::KOFF + PAR * TB;
-    const char* vs = lds + QLds<D>::VOFF + PAR * TB;
-    const uint32_t* mk = reinterpret_cast<const uint32_t*>(lds + QLds<D>::MOFF + PAR * Geo<D>::MBYTES);
-    const bool need = (c.blk[t] & c.bits) != c.bits;
+    const char* ks = st.k[PAR];
+    const char* vs = st.v[PAR];
+    const uint32_t* mk = reinterpret_cast<const uint32_t*>(st.m[PAR]);
+    const bool need = (blk & c.bits) != c.bits;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const f32x16 s = row_mfma<D>(c.q, ks, c.krow, kb);
@@ -161,11 +168,15 @@ __device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, char* 
   }
   wait_copies();
   __syncthreads();
+  blk = blk_next;
 }
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int total) {
-  __shared__ __align__(16) char lds[QLds<D>::SIZE];
+  __shared__ __align__(16) char lds_k0[Geo<D>::TILEB], lds_k1[Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_v0[Geo<D>::TILEB], lds_v1[Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_m0[Geo<D>::MBYTES], lds_m1[Geo<D>::MBYTES];
+  const QStages st = {{lds_k0, lds_k1}, {lds_v0, lds_v1}, {lds_m0, lds_m1}};
   const int G = gridDim.x;
   const int bid = blockIdx.x;
   const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
@@ -241,18 +252,19 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   const int nt = c.nt;
   if (nt > 0) {
     const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
-    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, i0, lds + QLds<D>::KOFF, c.wave);
-    copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, i0, lds + QLds<D>::VOFF, c.wave);
-    copy_dwords(c.kv_mask, lds + QLds<D>::MOFF, c.lane);
+    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, i0, st.k[0], c.wave);
+    copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, i0, st.v[0], c.wave);
+    copy_dwords(c.kv_mask, st.m[0], c.lane);
     Idx<D> inext = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
+    uint32_t blk = c.blk[0];
     wait_copies();
     __syncthreads();
     int t = 0;
     for (; t + 1 < nt; t += 2) {
-      dq_tile<D, 0>(c, t, inext, lds);
-      dq_tile<D, 1>(c, t + 1, inext, lds);
+      dq_tile<D, 0>(c, t, inext, blk, st);
+      dq_tile<D, 1>(c, t + 1, inext, blk, st);
     }
-    if (t < nt) dq_tile<D, 0>(c, t, inext, lds);
+    if (t < nt) dq_tile<D, 0>(c, t, inext, blk, st);
   }
   if (c.active && c.valid)
     store_acc<D>(a.dq + (int64_t)c.qtok * a.dq_ss + (int64_t)head * a.dq_sh, c.dq, a.scale, c.lane);
@@ -260,13 +272,12 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
 
 // ---- dK, dV (key-major) ------------------------------------------------------
 
-// LDS: Q[2] | dO[2] (rows and transposed) | per-query dwords[2] x {mask, lse2, delta}
-template <int D>
-struct KLds {
-  static constexpr int QOFF = 0;
-  static constexpr int DOFF = 2 * Geo<D>::TILEB;
-  static constexpr int WOFF = 4 * Geo<D>::TILEB;            // + stage * 3 * MBYTES
-  static constexpr int SIZE = 4 * Geo<D>::TILEB + 6 * Geo<D>::MBYTES;
+// LDS stages: Q[2] | dO[2] (rows and transposed) | per-query dwords[2] x
+// {mask, lse2, delta}, each stage its own __shared__ array (see QStages).
+struct KStages {
+  char* q[2];
+  char* d[2];
+  char* w[2];
 };
 
 template <int D>
@@ -305,20 +316,18 @@ __device__ __forceinline__ void kdv_copy(KCtx<D>& c, int t, const Idx<D>& ix, in
 }
 
 template <int D, int PAR>
-__device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int& qnext, char* lds) {
-  constexpr int TB = Geo<D>::TILEB;
-  constexpr int WB = 3 * Geo<D>::MBYTES;
+__device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int& qnext,
+                                          const KStages& st) {
   if (t + 1 < c.nt) {
-    kdv_copy<D>(c, t + 1, inext, qnext, lds + KLds<D>::QOFF + (PAR ^ 1) * TB,
-                lds + KLds<D>::DOFF + (PAR ^ 1) * TB, lds + KLds<D>::WOFF + (PAR ^ 1) * WB);
+    kdv_copy<D>(c, t + 1, inext, qnext, st.q[PAR ^ 1], st.d[PAR ^ 1], st.w[PAR ^ 1]);
     const int tn = min(t + 2, c.nt - 1);
     inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
     qnext = c.q_idx[tn * kSlab + c.lane];
   }
   if (c.active) {
-    const char* qs = lds + KLds<D>::QOFF + PAR * TB;
-    const char* ds_ = lds + KLds<D>::DOFF + PAR * TB;
-    const char* ws = lds + KLds<D>::WOFF + PAR * WB;
+    const char* qs = st.q[PAR];
+    const char* ds_ = st.d[PAR];
+    const char* ws = st.w[PAR];
     const uint32_t* mk = reinterpret_cast<const uint32_t*>(ws);
     const float* l2 = reinterpret_cast<const float*>(ws + Geo<D>::MBYTES);
     const float* dl = reinterpret_cast<const float*>(ws + 2 * Geo<D>::MBYTES);
@@ -354,7 +363,10 @@ __device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int&
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int total) {
-  __shared__ __align__(16) char lds[KLds<D>::SIZE];
+  __shared__ __align__(16) char lds_q0[Geo<D>::TILEB], lds_q1[Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_d0[Geo<D>::TILEB], lds_d1[Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_w0[3 * Geo<D>::MBYTES], lds_w1[3 * Geo<D>::MBYTES];
+  const KStages st = {{lds_q0, lds_q1}, {lds_d0, lds_d1}, {lds_w0, lds_w1}};
   const int G = gridDim.x;
   const int bid = blockIdx.x;
   const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
@@ -407,8 +419,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int to
   const int nt = c.nt;
   if (nt > 0) {
     const Idx<D> i0 = load_idx<D>(c.q_idx, 0, c.cq.idx_off);
-    kdv_copy<D>(c, 0, i0, c.q_idx[c.lane], lds + KLds<D>::QOFF, lds + KLds<D>::DOFF,
-                lds + KLds<D>::WOFF);
+    kdv_copy<D>(c, 0, i0, c.q_idx[c.lane], st.q[0], st.d[0], st.w[0]);
     const int tn = min(1, nt - 1);
     Idx<D> inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
     int qnext = c.q_idx[tn * kSlab + c.lane];
@@ -416,10 +427,10 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int to
     __syncthreads();
     int t = 0;
     for (; t + 1 < nt; t += 2) {
-      dkdv_tile<D, 0>(c, t, inext, qnext, lds);
-      dkdv_tile<D, 1>(c, t + 1, inext, qnext, lds);
+      dkdv_tile<D, 0>(c, t, inext, qnext, st);
+      dkdv_tile<D, 1>(c, t + 1, inext, qnext, st);
     }
-    if (t < nt) dkdv_tile<D, 0>(c, t, inext, qnext, lds);
+    if (t < nt) dkdv_tile<D, 0>(c, t, inext, qnext, st);
   }
   if (c.active && c.valid) {
     store_acc<D>(a.dk + (int64_t)c.ktok * a.dk_ss + (int64_t)head * a.dk_sh, c.dk, a.scale, c.lane);
