@@ -12,14 +12,18 @@
 // with the same bf16 rounding points as the reference.  The reference rotates
 // in float64; here the rotation runs in fp32 from fp32 cos/sin tables, so a
 // result can differ from the reference by one bf16 ulp.  The RMS spans all
-// heads (the full model dim), so one workgroup owns whole tokens: dim/8
-// threads x 8 channels.  Camera weights stay in registers while the
-// workgroup walks kTokens tokens.  V is copied into the requested layout.
+// heads (the full model dim), so one workgroup owns whole tokens: dim/CPT
+// threads x CPT channels (CPT = 4 up to dim 3072, else 8).  Camera weights
+// stay in registers, packed, while the workgroup walks kTokens tokens two at a
+// time: one workgroup reduction serves both tokens, each unpacked weight feeds
+// both, and the next two tokens' projections and camera rows are loaded while
+// the current two are computed.  V is copied into the requested layout.
 #include "hier_common.h"
 
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kTokens = 32;
 
 __device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
@@ -28,34 +32,60 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
-// Sum over the workgroup; blockDim is a multiple of 64 or a power of two below 64.
-__device__ __forceinline__ float2 block_sum2(float2 v, float2* red) {
+// Sums of NV values over the workgroup (blockDim a multiple of 64 or a power
+// of two below 64); red holds 16 waves x NV partial sums.
+template <int NV>
+__device__ __forceinline__ void block_sum(float* v, float* red) {
   const int width = blockDim.x < 64 ? (int)blockDim.x : 64;
-  for (int d = 1; d < width; d <<= 1) {
-    v.x += __shfl_xor(v.x, d, 64);
-    v.y += __shfl_xor(v.y, d, 64);
-  }
+  for (int d = 1; d < width; d <<= 1)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] += __shfl_xor(v[i], d, 64);
   const int nw = (blockDim.x + 63) >> 6;
   const int w = threadIdx.x >> 6;
+  __syncthreads();   // the previous sums have been read
+  if ((threadIdx.x & 63) == 0)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) red[w * NV + i] = v[i];
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float2 t = make_float2(0.f, 0.f);
-  for (int i = 0; i < nw; ++i) { t.x += red[i].x; t.y += red[i].y; }
-  return t;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float t = 0.f;
+    for (int ww = 0; ww < nw; ++ww) t += red[ww * NV + i];
+    v[i] = t;
+  }
 }
 
-template <int C>
-__global__ __launch_bounds__(512) void prologue_kernel(HierPrologueArgs a) {
-  __shared__ float2 red[16];
+// The inputs of one token that the camera / norm stage needs first (loaded a
+// trip ahead); V and the RoPE tables are loaded at the start of the trip that
+// uses them.
+// CPT channels per thread: 4 for model dims up to 3072 (more waves per CU:
+// the camera weights held per thread halve), 8 up to 4096.
+template <int CPT>
+struct Chw;
+template <>
+struct Chw<4> { typedef u32x2 type; };
+template <>
+struct Chw<8> { typedef u32x4 type; };
+
+template <int C, int CPT>
+struct TokIn {
+  typename Chw<CPT>::type q4, k4;
+  u32x2 cam[C > 0 ? C / 4 : 1];   // C bf16 = C / 4 pairs of packed words
+};
+
+template <int C, int kCPT>
+__global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPrologueArgs a) {
+  typedef typename Chw<kCPT>::type chw_t;
+  __shared__ float red[16 * 4];
   const int dim = a.H * a.D;
-  const int c0 = threadIdx.x * 8;           // first channel of this thread
+  const int c0 = threadIdx.x * kCPT;        // first channel of this thread
   const int head = c0 / a.D, d0 = c0 - head * a.D;
   const int half = a.D / 2;
+  const int m0 = d0 / 2;
 
-  // camera weights of this thread's 8 channels: rows c0..c0+7 of [dim][C] are
+  // camera weights of this thread's kCPT channels: rows c0.. of [dim][C] are
   // contiguous, loaded as packed bf16 pairs (word i = elements 2i, 2i+1)
-  constexpr int NW = C > 0 ? 8 * C / 8 : 1;     // 16-byte vectors
+  constexpr int NW = C > 0 ? kCPT * C / 8 : 1;     // 16-byte vectors
   u32x4 wq[NW], wk[NW];
   if constexpr (C > 0) {
 #pragma unroll
@@ -64,29 +94,61 @@ __global__ __launch_bounds__(512) void prologue_kernel(HierPrologueArgs a) {
       wk[i] = *reinterpret_cast<const u32x4*>(a.w_cam_k + (int64_t)c0 * C + 8 * i);
     }
   }
-  float gq[8], gk[8];
+  float gq[kCPT], gk[kCPT];
   {
-    const u32x4 q4 = *reinterpret_cast<const u32x4*>(a.norm_q_w + c0);
-    const u32x4 k4 = *reinterpret_cast<const u32x4*>(a.norm_k_w + c0);
+    const chw_t q4 = *reinterpret_cast<const chw_t*>(a.norm_q_w + c0);
+    const chw_t k4 = *reinterpret_cast<const chw_t*>(a.norm_k_w + c0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < kCPT / 2; ++e) {
       gq[2 * e] = bf2f(q4[e] & 0xffffu); gq[2 * e + 1] = bf2f(q4[e] >> 16);
       gk[2 * e] = bf2f(k4[e] & 0xffffu); gk[2 * e + 1] = bf2f(k4[e] >> 16);
     }
   }
-
-  const int s_end = min(a.S, (int)(blockIdx.x + 1) * kTokens);
-  for (int s = blockIdx.x * kTokens; s < s_end; ++s) {
-    float q[8], k[8];
-    {
-      const u32x4 q4 = *reinterpret_cast<const u32x4*>(a.qx + (int64_t)s * dim + c0);
-      const u32x4 k4 = *reinterpret_cast<const u32x4*>(a.kx + (int64_t)s * dim + c0);
+  auto load = [&](int s) {
+    TokIn<C, kCPT> x;
+    x.q4 = *reinterpret_cast<const chw_t*>(a.qx + (int64_t)s * dim + c0);
+    x.k4 = *reinterpret_cast<const chw_t*>(a.kx + (int64_t)s * dim + c0);
+    if constexpr (C > 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        q[2 * e] = bf2f(q4[e] & 0xffffu); q[2 * e + 1] = bf2f(q4[e] >> 16);
-        k[2 * e] = bf2f(k4[e] & 0xffffu); k[2 * e + 1] = bf2f(k4[e] >> 16);
-      }
+      for (int i = 0; i < C / 4; ++i)
+        x.cam[i] = *reinterpret_cast<const u32x2*>(a.cam + (int64_t)s * C + 4 * i);
     }
+    return x;
+  };
+
+  // Two tokens per trip (one reduction for both, each unpacked camera weight
+  // feeds both), the next two tokens' inputs loaded during the current ones.
+  // An odd last token is paired with itself and stored once.
+  const int s_begin = blockIdx.x * kTokens;
+  const int s_end = min(a.S, s_begin + kTokens);
+  TokIn<C, kCPT> n0 = load(s_begin), n1 = load(min(s_begin + 1, s_end - 1));
+  for (int s = s_begin; s < s_end; s += 2) {
+    const TokIn<C, kCPT> x[2] = {n0, n1};
+    const bool second = s + 1 < s_end;
+    const int s1 = second ? s + 1 : s;
+    typedef float rope_t __attribute__((ext_vector_type(kCPT / 2)));
+    rope_t cs[2], sn[2];
+    chw_t v4[2];
+    cs[0] = *reinterpret_cast<const rope_t*>(a.rope_cos + (int64_t)s * half + m0);
+    sn[0] = *reinterpret_cast<const rope_t*>(a.rope_sin + (int64_t)s * half + m0);
+    cs[1] = *reinterpret_cast<const rope_t*>(a.rope_cos + (int64_t)s1 * half + m0);
+    sn[1] = *reinterpret_cast<const rope_t*>(a.rope_sin + (int64_t)s1 * half + m0);
+    if (a.v_out) {
+      v4[0] = *reinterpret_cast<const chw_t*>(a.vx + (int64_t)s * dim + c0);
+      v4[1] = *reinterpret_cast<const chw_t*>(a.vx + (int64_t)s1 * dim + c0);
+    }
+    if (s + 2 < s_end) {
+      n0 = load(s + 2);
+      n1 = load(min(s + 3, s_end - 1));
+    }
+    float q[2][kCPT], k[2][kCPT];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < kCPT / 2; ++e) {
+        q[t][2 * e] = bf2f(x[t].q4[e] & 0xffffu); q[t][2 * e + 1] = bf2f(x[t].q4[e] >> 16);
+        k[t][2 * e] = bf2f(x[t].k4[e] & 0xffffu); k[t][2 * e + 1] = bf2f(x[t].k4[e] >> 16);
+      }
     if constexpr (C > 0) {
       // keep the weights packed: stops the unpack being hoisted out of the
       // token loop (it would need 2*8*C fp32 registers)
@@ -95,61 +157,76 @@ __global__ __launch_bounds__(512) void prologue_kernel(HierPrologueArgs a) {
         asm volatile("" : "+v"(wq[i]));
         asm volatile("" : "+v"(wk[i]));
       }
-      float cam[C];
+      float cam[2][C];
 #pragma unroll
-      for (int c = 0; c < C; ++c) cam[c] = bf2f(a.cam[(int64_t)s * C + c]);
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float aq = 0.f, ak = 0.f;
+        for (int i = 0; i < C / 4; ++i)
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            cam[t][4 * i + 2 * w] = bf2f(x[t].cam[i][w] & 0xffffu);
+            cam[t][4 * i + 2 * w + 1] = bf2f(x[t].cam[i][w] >> 16);
+          }
+#pragma unroll
+      for (int e = 0; e < kCPT; ++e) {
+        float aq[2] = {0.f, 0.f}, ak[2] = {0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < C / 2; ++c) {
           const int w = (e * C) / 2 + c;     // packed word of elements (e, 2c), (e, 2c+1)
           const uint32_t xq = wq[w >> 2][w & 3], xk = wk[w >> 2][w & 3];
-          aq = fmaf(cam[2 * c], __uint_as_float(xq << 16), aq);
-          aq = fmaf(cam[2 * c + 1], __uint_as_float(xq & 0xffff0000u), aq);
-          ak = fmaf(cam[2 * c], __uint_as_float(xk << 16), ak);
-          ak = fmaf(cam[2 * c + 1], __uint_as_float(xk & 0xffff0000u), ak);
+          const float wq0 = __uint_as_float(xq << 16), wq1 = __uint_as_float(xq & 0xffff0000u);
+          const float wk0 = __uint_as_float(xk << 16), wk1 = __uint_as_float(xk & 0xffff0000u);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            aq[t] = fmaf(cam[t][2 * c], wq0, aq[t]);
+            aq[t] = fmaf(cam[t][2 * c + 1], wq1, aq[t]);
+            ak[t] = fmaf(cam[t][2 * c], wk0, ak[t]);
+            ak[t] = fmaf(cam[t][2 * c + 1], wk1, ak[t]);
+          }
         }
-        q[e] = rbf(q[e] + rbf(aq));
-        k[e] = rbf(k[e] + rbf(ak));
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          q[t][e] = rbf(q[t][e] + rbf(aq[t]));
+          k[t][e] = rbf(k[t][e] + rbf(ak[t]));
+        }
       }
     }
-    float2 ss = make_float2(0.f, 0.f);
+    float ss[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ss.x = fmaf(q[e], q[e], ss.x);
-      ss.y = fmaf(k[e], k[e], ss.y);
-    }
-    ss = block_sum2(ss, red);
-    const float iq = rsqrtf(ss.x / (float)dim + a.eps);
-    const float ik = rsqrtf(ss.y / (float)dim + a.eps);
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      q[e] = rbf(rbf(q[e] * iq) * gq[e]);
-      k[e] = rbf(rbf(k[e] * ik) * gk[e]);
-    }
-    // RoPE on (even, odd) channel pairs of this head
-    uint32_t qo[4], ko[4];
+      for (int e = 0; e < kCPT; ++e) {
+        ss[2 * t] = fmaf(q[t][e], q[t][e], ss[2 * t]);
+        ss[2 * t + 1] = fmaf(k[t][e], k[t][e], ss[2 * t + 1]);
+      }
+    block_sum<4>(ss, red);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = d0 / 2 + e;
-      const float cs = a.rope_cos[(int64_t)s * half + m];
-      const float sn = a.rope_sin[(int64_t)s * half + m];
-      const float qr = q[2 * e] * cs - q[2 * e + 1] * sn;
-      const float qi = q[2 * e] * sn + q[2 * e + 1] * cs;
-      const float kr = k[2 * e] * cs - k[2 * e + 1] * sn;
-      const float ki = k[2 * e] * sn + k[2 * e + 1] * cs;
-      qo[e] = f2bf(qr) | (f2bf(qi) << 16);
-      ko[e] = f2bf(kr) | (f2bf(ki) << 16);
+    for (int t = 0; t < 2; ++t) {
+      if (t == 1 && !second) break;
+      const float iq = rsqrtf(ss[2 * t] / (float)dim + a.eps);
+      const float ik = rsqrtf(ss[2 * t + 1] / (float)dim + a.eps);
+#pragma unroll
+      for (int e = 0; e < kCPT; ++e) {
+        q[t][e] = rbf(rbf(q[t][e] * iq) * gq[e]);
+        k[t][e] = rbf(rbf(k[t][e] * ik) * gk[e]);
+      }
+      // RoPE on (even, odd) channel pairs of this head
+      chw_t qv, kv;
+#pragma unroll
+      for (int e = 0; e < kCPT / 2; ++e) {
+        const float c = cs[t][e], sv = sn[t][e];
+        const float qr = q[t][2 * e] * c - q[t][2 * e + 1] * sv;
+        const float qi = q[t][2 * e] * sv + q[t][2 * e + 1] * c;
+        const float kr = k[t][2 * e] * c - k[t][2 * e + 1] * sv;
+        const float ki = k[t][2 * e] * sv + k[t][2 * e + 1] * c;
+        qv[e] = f2bf(qr) | (f2bf(qi) << 16);
+        kv[e] = f2bf(kr) | (f2bf(ki) << 16);
+      }
+      const int64_t off = (int64_t)(s + t) * a.out_stride_s + (int64_t)head * a.out_stride_h + d0;
+      *reinterpret_cast<chw_t*>(a.q_out + off) = qv;
+      *reinterpret_cast<chw_t*>(a.k_out + off) = kv;
+      if (a.v_out) *reinterpret_cast<chw_t*>(a.v_out + off) = v4[t];
     }
-    const int64_t off = (int64_t)s * a.out_stride_s + (int64_t)head * a.out_stride_h + d0;
-    u32x4 qv = {qo[0], qo[1], qo[2], qo[3]};
-    u32x4 kv = {ko[0], ko[1], ko[2], ko[3]};
-    *reinterpret_cast<u32x4*>(a.q_out + off) = qv;
-    *reinterpret_cast<u32x4*>(a.k_out + off) = kv;
-    if (a.v_out)
-      *reinterpret_cast<u32x4*>(a.v_out + off) =
-          *reinterpret_cast<const u32x4*>(a.vx + (int64_t)s * dim + c0);
   }
 }
 
@@ -162,25 +239,35 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   HIER_REQUIRE(a.S >= 0 && a.H >= 1 && (a.D == 64 || a.D == 128), HIER_EUNSUPPORTED,
                "prologue supports head_dim 64/128, got H=%d D=%d", a.H, a.D);
   const int dim = a.H * a.D;
-  const int nthr = dim / 8;
-  HIER_REQUIRE(dim % 8 == 0 && nthr <= 512 && nthr >= 8 &&
+  const int kCPT = dim <= 3072 ? 4 : 8;
+  const int nthr = dim / kCPT;
+  HIER_REQUIRE(dim % kCPT == 0 && nthr <= (kCPT == 4 ? 768 : 512) && nthr >= 8 &&
                    (nthr % 64 == 0 || (nthr < 64 && (nthr & (nthr - 1)) == 0)),
-               HIER_EUNSUPPORTED, "model dim %d must be 8 x (a multiple of 64 up to 512, or a power of two)",
+               HIER_EUNSUPPORTED,
+               "model dim %d must be a multiple of 256 up to 3072, of 512 up to 4096, or a power "
+               "of two of at least 32",
                dim);
   HIER_REQUIRE(a.qx && a.kx && a.norm_q_w && a.norm_k_w && a.rope_cos && a.rope_sin && a.q_out &&
                    a.k_out && (!a.v_out || a.vx),
                HIER_EINVAL, "NULL tensor pointer");
-  HIER_REQUIRE(a.out_stride_s % 8 == 0 && a.out_stride_h % 8 == 0, HIER_EINVAL,
-               "output strides must keep 16-byte alignment");
+  HIER_REQUIRE(a.out_stride_s % kCPT == 0 && a.out_stride_h % kCPT == 0, HIER_EINVAL,
+               "output strides must keep %d-byte alignment", 2 * kCPT);
   const bool cam = a.cam != nullptr;
   HIER_REQUIRE(!cam || (a.C == 12 && a.w_cam_q && a.w_cam_k), HIER_EUNSUPPORTED,
                "camera adapter supports C=12 with both weights, got C=%d", a.C);
+  HIER_REQUIRE(((uintptr_t)a.rope_cos & 15u) == 0 && ((uintptr_t)a.rope_sin & 15u) == 0 &&
+                   (!cam || ((uintptr_t)a.cam & 7u) == 0),
+               HIER_EINVAL, "RoPE tables must be 16-byte and camera rows 8-byte aligned");
   if (a.S == 0) return HIER_OK;
   const int grid = (a.S + kTokens - 1) / kTokens;
-  const int threads = dim / 8;
-  if (cam)
-    hipLaunchKernelGGL(prologue_kernel<12>, dim3(grid), dim3(threads), 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(prologue_kernel<0>, dim3(grid), dim3(threads), 0, (hipStream_t)stream, a);
+  const int threads = nthr;
+  const hipStream_t st = (hipStream_t)stream;
+  if (kCPT == 4) {
+    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 4>), dim3(grid), dim3(threads), 0, st, a);
+    else hipLaunchKernelGGL((prologue_kernel<0, 4>), dim3(grid), dim3(threads), 0, st, a);
+  } else {
+    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 8>), dim3(grid), dim3(threads), 0, st, a);
+    else hipLaunchKernelGGL((prologue_kernel<0, 8>), dim3(grid), dim3(threads), 0, st, a);
+  }
   return hier::check_launch("prologue_kernel");
 }
