@@ -14,11 +14,15 @@
 //               dQ^T += K^T dS^T      (K transposed out of LDS)
 //             Also writes delta and lse2 = lse * log2(e) per query row.
 // dkdv_kernel key-major, over the transposed tile list (128 key rows per
-//             item, lists of query rows with a bitmask over key frames).  Per
-//             32-query block:
-//               S  = Q K^T,  dP = dO V^T   (Q / dO rows from LDS, K^T / V^T
-//                                           in registers)
-//               dV^T += dO^T P,  dK^T += Q^T dS   (Q / dO transposed out of LDS)
+//             item, lists of query rows with a bitmask over key frames), in
+//             two passes so that each runs two waves per SIMD (one wave owning
+//             both the dK and the dV accumulators needs more than the 256
+//             registers of two waves, and one wave per SIMD is VALU-issue
+//             bound here).  Per 32-query block:
+//               pass dV: S = Q K^T, P;  dV^T += dO^T P
+//               pass dK: S = Q K^T, dP = dO V^T, dS;  dK^T += Q^T dS
+//             (Q / dO rows from LDS, K^T / V^T in registers, Q / dO
+//             transposed out of LDS for the accumulation).
 // The lane layouts are the forward's: an MFMA result keeps one column per
 // lane and its rows {8*(r/4) + 4*(lane/32) + r%4}, which is exactly the
 // permuted k order of the next MFMA's register operand, so P and dS go from
@@ -295,15 +299,17 @@ struct KCtx {
   bool active;
   Copier<D, kBothRead> cq;
   int row[Geo<D>::NC], tr[Geo<D>::NDB][2];
-  // key rows
+  // key rows (vt: pass dK only) and the pass's accumulator (dV^T or dK^T)
   bf16x8 kt[Geo<D>::NC], vt[Geo<D>::NC];
-  f32x16 dk[Geo<D>::NDB], dv[Geo<D>::NDB];
+  f32x16 acc[Geo<D>::NDB];
   int ktok, kframe;
   bool valid;
   uint32_t bits;
 };
 
-template <int D>
+constexpr int kPassDV = 0, kPassDK = 1;
+
+template <int D, int PASS>
 __device__ __forceinline__ void kdv_copy(KCtx<D>& c, int t, const Idx<D>& ix, int qtok, char* stage_q,
                                          char* stage_do, char* stage_w) {
   copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, ix, stage_q, c.wave);
@@ -311,15 +317,16 @@ __device__ __forceinline__ void kdv_copy(KCtx<D>& c, int t, const Idx<D>& ix, in
   copy_dwords(c.q_mask + t * kSlab, stage_w, c.lane);
   __builtin_amdgcn_global_load_lds((gbl_void*)(c.lse2 + qtok), (lds_void*)(stage_w + Geo<D>::MBYTES),
                                    4, 0, 0);
-  __builtin_amdgcn_global_load_lds((gbl_void*)(c.delta + qtok),
-                                   (lds_void*)(stage_w + 2 * Geo<D>::MBYTES), 4, 0, 0);
+  if constexpr (PASS == kPassDK)
+    __builtin_amdgcn_global_load_lds((gbl_void*)(c.delta + qtok),
+                                     (lds_void*)(stage_w + 2 * Geo<D>::MBYTES), 4, 0, 0);
 }
 
-template <int D, int PAR>
+template <int D, int PASS, int PAR>
 __device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int& qnext,
                                           const KStages& st) {
   if (t + 1 < c.nt) {
-    kdv_copy<D>(c, t + 1, inext, qnext, st.q[PAR ^ 1], st.d[PAR ^ 1], st.w[PAR ^ 1]);
+    kdv_copy<D, PASS>(c, t + 1, inext, qnext, st.q[PAR ^ 1], st.d[PAR ^ 1], st.w[PAR ^ 1]);
     const int tn = min(t + 2, c.nt - 1);
     inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
     qnext = c.q_idx[tn * kSlab + c.lane];
@@ -334,35 +341,40 @@ __device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int&
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const f32x16 s = row_mfma<D>(c.kt, qs, c.row, qb);
-      const f32x16 dp = row_mfma<D>(c.vt, ds_, c.row, qb);
-      bf16x8 pb[2], dsb[2];
+      f32x16 dp;
+      if constexpr (PASS == kPassDK) dp = row_mfma<D>(c.vt, ds_, c.row, qb);
+      bf16x8 ob[2];   // P (pass dV) or dS (pass dK), bf16
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
         const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[q0]);
         const u32x4 lw = *reinterpret_cast<const u32x4*>(&l2[q0]);
-        const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
+        u32x4 dw;
+        if constexpr (PASS == kPassDK) dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * g4 + e;
           const uint32_t keep = keep_mask(w[e], c.kframe);
           const float p = __uint_as_float(
               __float_as_uint(__builtin_amdgcn_exp2f(fmaf(s[i], c.c2, -__uint_as_float(lw[e])))) & keep);
-          const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - __uint_as_float(dw[e]))) & keep);
-          pb[i >> 3][i & 7] = (__bf16)p;
-          dsb[i >> 3][i & 7] = (__bf16)ds;
+          if constexpr (PASS == kPassDV) {
+            ob[i >> 3][i & 7] = (__bf16)p;
+          } else {
+            const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - __uint_as_float(dw[e]))) & keep);
+            ob[i >> 3][i & 7] = (__bf16)ds;
+          }
         }
       }
-      tr_mfma<D>(c.dv, pb, ds_, c.tr, qb);
-      tr_mfma<D>(c.dk, dsb, qs, c.tr, qb);
+      // dV^T += dO^T P  /  dK^T += Q^T dS
+      tr_mfma<D>(c.acc, ob, PASS == kPassDV ? ds_ : qs, c.tr, qb);
     }
   }
   wait_copies();
   __syncthreads();
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int total) {
+template <int D, int PASS>
+__global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(HierBwdArgs a, int total) {
   __shared__ __align__(16) char lds_q0[Geo<D>::TILEB], lds_q1[Geo<D>::TILEB];
   __shared__ __align__(16) char lds_d0[Geo<D>::TILEB], lds_d1[Geo<D>::TILEB];
   __shared__ __align__(16) char lds_w0[3 * Geo<D>::MBYTES], lds_w1[3 * Geo<D>::MBYTES];
@@ -410,16 +422,17 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int to
   c.ktok = kbase + c.kframe * kstride + (ri - c.kframe * klen);
   c.bits = wave_or(c.valid ? (1u << c.kframe) : 0u);
   load_row<D>(c.kt, a.k + (int64_t)c.ktok * a.k_ss + (int64_t)head * a.k_sh, c.lane);
-  load_row<D>(c.vt, a.v + (int64_t)c.ktok * a.v_ss + (int64_t)head * a.v_sh, c.lane);
+  if constexpr (PASS == kPassDK)
+    load_row<D>(c.vt, a.v + (int64_t)c.ktok * a.v_ss + (int64_t)head * a.v_sh, c.lane);
 #pragma unroll
   for (int db = 0; db < Geo<D>::NDB; ++db)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) c.dk[db][i] = c.dv[db][i] = 0.f;
+    for (int i = 0; i < 16; ++i) c.acc[db][i] = 0.f;
 
   const int nt = c.nt;
   if (nt > 0) {
     const Idx<D> i0 = load_idx<D>(c.q_idx, 0, c.cq.idx_off);
-    kdv_copy<D>(c, 0, i0, c.q_idx[c.lane], st.q[0], st.d[0], st.w[0]);
+    kdv_copy<D, PASS>(c, 0, i0, c.q_idx[c.lane], st.q[0], st.d[0], st.w[0]);
     const int tn = min(1, nt - 1);
     Idx<D> inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
     int qnext = c.q_idx[tn * kSlab + c.lane];
@@ -427,14 +440,16 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_kernel(HierBwdArgs a, int to
     __syncthreads();
     int t = 0;
     for (; t + 1 < nt; t += 2) {
-      dkdv_tile<D, 0>(c, t, inext, qnext, st);
-      dkdv_tile<D, 1>(c, t + 1, inext, qnext, st);
+      dkdv_tile<D, PASS, 0>(c, t, inext, qnext, st);
+      dkdv_tile<D, PASS, 1>(c, t + 1, inext, qnext, st);
     }
-    if (t < nt) dkdv_tile<D, 0>(c, t, inext, qnext, st);
+    if (t < nt) dkdv_tile<D, PASS, 0>(c, t, inext, qnext, st);
   }
   if (c.active && c.valid) {
-    store_acc<D>(a.dk + (int64_t)c.ktok * a.dk_ss + (int64_t)head * a.dk_sh, c.dk, a.scale, c.lane);
-    store_acc<D>(a.dv + (int64_t)c.ktok * a.dv_ss + (int64_t)head * a.dv_sh, c.dv, 1.f, c.lane);
+    if constexpr (PASS == kPassDK)
+      store_acc<D>(a.dk + (int64_t)c.ktok * a.dk_ss + (int64_t)head * a.dk_sh, c.acc, a.scale, c.lane);
+    else
+      store_acc<D>(a.dv + (int64_t)c.ktok * a.dv_ss + (int64_t)head * a.dv_sh, c.acc, 1.f, c.lane);
   }
 }
 
@@ -604,10 +619,13 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
   }
   if (tk > 0) {
     const int grid = (int)((tk + 7) / 8 * 8);
-    if (a.D == 128)
-      hipLaunchKernelGGL(dkdv_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
-    else
-      hipLaunchKernelGGL(dkdv_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
+    if (a.D == 128) {
+      hipLaunchKernelGGL((dkdv_kernel<128, kPassDV>), dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
+      hipLaunchKernelGGL((dkdv_kernel<128, kPassDK>), dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
+    } else {
+      hipLaunchKernelGGL((dkdv_kernel<64, kPassDV>), dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
+      hipLaunchKernelGGL((dkdv_kernel<64, kPassDK>), dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
+    }
     int rc = hier::check_launch("dkdv_kernel");
     if (rc != HIER_OK) return rc;
   }
