@@ -1,6 +1,6 @@
 """Benchmark: hierarchical-attention forward on one MI355X.
 
-Workload ("Wan2.2-5B-shaped layer"): 4 players x 42 latent
+Workload (configuration C2, a "Wan2.2-5B-shaped layer"): 4 players x 42 latent
 frames x 220 tokens, groups {0,1},{2,3} fixed, K_L=5 local and K_G=6 global hub
 tokens per frame, n=3 frames per causal block, window W=21, 24 heads x 128,
 bf16, q/k/v ~ 0.5 N(0,1) (synthetic).  One "step" is one full-sequence forward
@@ -12,7 +12,7 @@ reported separately, as is the fused Q/K prologue.
 Prints one JSON line (the driver contract).  ``--config p6|c3|p10|...`` makes
 another full-sequence configuration the headline line.  Unless ``--no-suite``,
 the line's ``extra.suite`` also carries, from the same run: the forward at 6, 8
-and 10 players; the training step of BASELINE config C5 (forward + backward +
+and 10 players; the training step of configuration C5 (forward + backward +
 membership STE, P=4, T=21, W=7); and the per-chunk latency of the cached
 rollout of config C4 (10 players, chunks of 6 frames through the paged KV
 cache, steady state of the denoising passes).

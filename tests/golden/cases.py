@@ -3,7 +3,7 @@
 Each case is a plain JSON-serialisable dict of builder inputs.  The shapes
 follow the reference's own metadata tests
 (tests/test_hier_segmented_metadata.py:111-174, tests/test_hier_tiled_layout.py:30-206,
-tests/test_hier_tiled_ste_kernel.py:24-60), the BASELINE configurations C1 and
+tests/test_hier_tiled_ste_kernel.py:24-60), the benchmark configurations C1 and
 C2, and the reference grouping fixtures (tests/fixtures/grouping/*.labels.npz,
 whose membership rows are copied into ``fixture_membership.npz`` as data).
 """
