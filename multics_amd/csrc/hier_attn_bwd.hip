@@ -315,11 +315,8 @@ __device__ __forceinline__ void kdv_copy(KCtx<D>& c, int t, const Idx<D>& ix, in
   copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, ix, stage_q, c.wave);
   copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, ix, stage_do, c.wave);
   copy_dwords(c.q_mask + t * kSlab, stage_w, c.lane);
-  __builtin_amdgcn_global_load_lds((gbl_void*)(c.lse2 + qtok), (lds_void*)(stage_w + Geo<D>::MBYTES),
-                                   4, 0, 0);
-  if constexpr (PASS == kPassDK)
-    __builtin_amdgcn_global_load_lds((gbl_void*)(c.delta + qtok),
-                                     (lds_void*)(stage_w + 2 * Geo<D>::MBYTES), 4, 0, 0);
+  dma4_lane(c.lse2 + qtok, stage_w + Geo<D>::MBYTES);
+  if constexpr (PASS == kPassDK) dma4_lane(c.delta + qtok, stage_w + 2 * Geo<D>::MBYTES);
 }
 
 template <int D, int PASS, int PAR>

@@ -269,14 +269,16 @@ __device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
     mask_block(sq, st.m[PAR ^ 1], B, R.qframe, c.lane);
 }
 
-// Tile iteration t (t + 1 < nt): copies K(t+2) + masks into stage PAR and
-// V(t+1) into stage PAR^1, loads the key indices and visibility flags of the
-// next iteration, runs half-steps 2t and 2t+1.  Invariant on entry: K(t+1),
-// masks(t+1) and V(t) resident; S(2t+1) (sb) masked; P(2t) (pa) ready with its
-// rescale pending; ik / iv / blk hold the indices of tiles min(t+2, nt-1) /
-// t+1 and the flags of tile t+1.  Every global load of the iteration is waited
-// for with the copies at its end, so nothing inside the half-steps waits on
-// the copies in flight.
+// Tile iteration t (t + 1 < nt): copies K(t+2) + masks into stage PAR, runs
+// half-step 2t, copies V(t+1) into stage PAR^1, runs half-step 2t+1; the key
+// indices and visibility flags of the next iteration are loaded on the way.
+// Both stages written are idle for the whole iteration; issuing the copies in
+// two bursts keeps a wave from stalling on a full memory queue with all eight
+// in flight.  Invariant on entry: K(t+1), masks(t+1) and V(t) resident;
+// S(2t+1) (sb) masked; P(2t) (pa) ready with its rescale pending; ik / iv /
+// blk hold the indices of tiles min(t+2, nt-1) / t+1 and the flags of tile
+// t+1.  Every global load of the iteration is waited for with the copies at
+// its end, so nothing inside the half-steps waits on the copies in flight.
 template <int D, int PAR>
 __device__ __forceinline__ void tile_iter(Ctx<D>& c, Rows<D>& R, int t, f32x16& sa, f32x16& sb,
                                           bf16x8* pa, bf16x8* pb, bool& resc, float& alpha_pend,
@@ -286,14 +288,12 @@ __device__ __forceinline__ void tile_iter(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
     if (c.wave == 0)
       copy_dwords(c.kv_mask + (t + 2) * kSlab, st.m[PAR], c.lane);
   }
-  copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, iv, st.v[PAR ^ 1], c.wave);
   ik = load_idx<D>(c.kv_idx, min(t + 3, c.nt - 1), c.ck.idx_off);
-  iv = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
   const uint32_t blk_pre = c.blk[min(t + 2, c.nt - 1)];
-  if (c.active) {
-    half_step<D, PAR, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, blk, st);
-    half_step<D, PAR, 1>(c, R, t, sb, sa, pb, pa, resc, alpha_pend, blk, st);
-  }
+  if (c.active) half_step<D, PAR, 0>(c, R, t, sa, sb, pa, pb, resc, alpha_pend, blk, st);
+  copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, iv, st.v[PAR ^ 1], c.wave);
+  iv = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+  if (c.active) half_step<D, PAR, 1>(c, R, t, sb, sa, pb, pa, resc, alpha_pend, blk, st);
   wait_copies();
   __syncthreads();
   blk = blk_pre;

@@ -31,8 +31,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef const __attribute__((address_space(1))) void gbl_void;
 
 constexpr int kSlab = 64;   // rows per LDS tile
 
@@ -129,19 +127,42 @@ __host__ __device__ constexpr bool copy_rows_ok(int64_t rows, int64_t row_stride
   return rows <= (1ll << 24) && row_stride_elems * 2 < (1ll << 24);
 }
 
+// The LDS DMA instructions are issued from inline assembly.  Issued through
+// the compiler builtin, an LDS DMA in flight makes the compiler wait for *all*
+// outstanding LDS reads (lgkmcnt(0)) before the first use of any of them, so a
+// wave could never keep more than the reads of one MFMA in flight while its
+// copies are pending -- which, with the copies overlapping the whole tile
+// iteration, is always.  Hidden in assembly the copies are invisible to that
+// bookkeeping; every copy is instead waited for explicitly (wait_copies, i.e.
+// vmcnt(0), then a workgroup barrier) before any LDS read of its stage.  The
+// LDS destination goes in M0 (set by the compiler through the "{m0}" operand;
+// the leading s_nop is the wait state between an M0 write and its use).  The
+// destination pointer must be wave-uniform.
+__device__ __forceinline__ void dma16(const char* gbase, uint32_t voff, const char* lds) {
+  const uint32_t l = (uint32_t)(uintptr_t)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(gbase), "{m0}"(l) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* gbase, uint32_t voff, const char* lds) {
+  const uint32_t l = (uint32_t)(uintptr_t)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(gbase), "{m0}"(l) : "memory");
+}
+// 4 bytes per lane from a per-lane 64-bit address.
+__device__ __forceinline__ void dma4_lane(const void* gaddr, const char* lds) {
+  const uint32_t l = (uint32_t)(uintptr_t)lds;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(gaddr), "{m0}"(l) : "memory");
+}
+
 // Copy e of one tile: 16 bytes per lane, 1 KB per wave instruction.  g points
 // at the head's first element of row 0 of the source tensor; rows are
-// addressed with 32-bit byte offsets.
+// addressed with 32-bit byte offsets (scalar base + 32-bit vector offset).
 template <int D, int S>
 __device__ __forceinline__ void copy_one(const char* g, uint32_t ss_bytes, const Copier<D, S>& cp,
                                          const Idx<D>& ix, int e, char* slot, int wave) {
-  uint32_t off = __umul24((uint32_t)ix.v[e], ss_bytes) + cp.add(e);
-  // opaque 32-bit offset: the copy then uses the scalar-base + 32-bit
-  // vector-offset address form instead of a 64-bit per-lane address
-  asm volatile("" : "+v"(off));
-  __builtin_amdgcn_global_load_lds(
-      (gbl_void*)(g + off), (lds_void*)(slot + (16 * wave + Geo<D>::NR * e) * Geo<D>::ROWB), 16, 0,
-      0);
+  const uint32_t off = __umul24((uint32_t)ix.v[e], ss_bytes) + cp.add(e);
+  dma16(g, off, slot + (16 * wave + Geo<D>::NR * e) * Geo<D>::ROWB);
 }
 
 template <int D, int S>
@@ -153,8 +174,7 @@ __device__ __forceinline__ void copy_tile(const char* g, uint32_t ss_bytes, cons
 
 // One dword per row of a tile (masks, per-row scalars), natural row order.
 __device__ __forceinline__ void copy_dwords(const void* m, char* slot, int lane) {
-  __builtin_amdgcn_global_load_lds((gbl_void*)(reinterpret_cast<const uint32_t*>(m) + lane),
-                                   (lds_void*)slot, 4, 0, 0);
+  dma4(m, 4u * (uint32_t)lane, slot);
 }
 
 __device__ __forceinline__ void wait_copies() {
