@@ -462,7 +462,7 @@ struct SLds {
   static constexpr int MOFF = 4 * Geo<D>::TILEB;
   static constexpr int COFF = MOFF + 2 * Geo<D>::MBYTES;
   static constexpr int AOFF = COFF + 2 * Geo<D>::MBYTES;
-  static constexpr int SIZE = AOFF + kWaves * 32 * kSteClasses * 4;
+  static constexpr int SIZE = AOFF + kSteClasses * kWaves * 32 * 4;
 };
 
 template <int D>
@@ -495,10 +495,15 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
 #pragma unroll
   for (int i = 0; i < Geo<D>::NC; ++i) roff[i] = row_read_off<D, kRowRead>(lane, i);
 
-  float* acc = reinterpret_cast<float*>(lds + SLds<D>::AOFF) + (wave * 32 + (lane & 31)) * kSteClasses;
+  // Per-query partial sums, one slot per (class, query row of the workgroup):
+  // acc[class * 128 + wave * 32 + (lane & 31)].  Only the two lanes of a query
+  // (its two key halves) share a slot, whatever the classes of the keys, so an
+  // add conflicts at most two ways.
+  constexpr int kSlots = kWaves * 32;
+  float* acc = reinterpret_cast<float*>(lds + SLds<D>::AOFF) + wave * 32 + (lane & 31);
   if (lane < 32)
 #pragma unroll
-    for (int cc = 0; cc < kSteClasses; ++cc) acc[cc] = 0.f;
+    for (int cc = 0; cc < kSteClasses; ++cc) acc[cc * kSlots] = 0.f;
 
   const int r = wave * 32 + (lane & 31);
   const bool valid = r < row_count;
@@ -511,22 +516,27 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
   const int64_t srow = (int64_t)head * a.lse_stride_h + qtok;
   const float lse2 = a.lse2[srow], delta = a.delta[srow];
 
+  // Tile t+1 is copied into the other stage while tile t is processed.
+  auto copy = [&](int t, const Idx<D>& ix) {
+    const int par = t & 1;
+    copy_tile<D, kRowRead>(gk, k_ss_b, cp, ix, lds + SLds<D>::KOFF + par * Geo<D>::TILEB, wave);
+    copy_tile<D, kRowRead>(gv, v_ss_b, cp, ix, lds + SLds<D>::VOFF + par * Geo<D>::TILEB, wave);
+    copy_dwords(kv_mask + t * kSlab, lds + SLds<D>::MOFF + par * Geo<D>::MBYTES, lane);
+    copy_dwords(kv_cls + t * kSlab, lds + SLds<D>::COFF + par * Geo<D>::MBYTES, lane);
+  };
+  if (nt > 0) copy(0, load_idx<D>(kv_idx, 0, cp.idx_off));
+  Idx<D> inext = load_idx<D>(kv_idx, min(1, max(nt - 1, 0)), cp.idx_off);
+  wait_copies();
+  __syncthreads();
   for (int t = 0; t < nt; ++t) {
     const int par = t & 1;
-    char* ks = lds + SLds<D>::KOFF + par * Geo<D>::TILEB;
-    char* vs = lds + SLds<D>::VOFF + par * Geo<D>::TILEB;
-    char* ms = lds + SLds<D>::MOFF + par * Geo<D>::MBYTES;
-    char* cs = lds + SLds<D>::COFF + par * Geo<D>::MBYTES;
-    const Idx<D> ix = load_idx<D>(kv_idx, t, cp.idx_off);
-    copy_tile<D, kRowRead>(gk, k_ss_b, cp, ix, ks, wave);
-    copy_tile<D, kRowRead>(gv, v_ss_b, cp, ix, vs, wave);
-    copy_dwords(kv_mask + t * kSlab, ms, lane);
-    copy_dwords(kv_cls + t * kSlab, cs, lane);
-    wait_copies();
-    __syncthreads();
+    if (t + 1 < nt) copy(t + 1, inext);
+    inext = load_idx<D>(kv_idx, min(t + 2, nt - 1), cp.idx_off);
+    const char* ks = lds + SLds<D>::KOFF + par * Geo<D>::TILEB;
+    const char* vs = lds + SLds<D>::VOFF + par * Geo<D>::TILEB;
+    const uint32_t* mk = reinterpret_cast<const uint32_t*>(lds + SLds<D>::MOFF + par * Geo<D>::MBYTES);
+    const int32_t* ck = reinterpret_cast<const int32_t*>(lds + SLds<D>::COFF + par * Geo<D>::MBYTES);
     if (active) {
-      const uint32_t* mk = reinterpret_cast<const uint32_t*>(ms);
-      const int32_t* ck = reinterpret_cast<const int32_t*>(cs);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const f32x16 s = row_mfma<D>(q, ks, roff, kb);
@@ -542,18 +552,19 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
             const float p = __builtin_amdgcn_exp2f(fmaf(s[i], c2, -lse2));
             const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - delta)) &
                                              keep_mask(w[e], qframe));
-            if (valid) atomicAdd(&acc[cl[e] & (kSteClasses - 1)], ds);
+            if (valid) atomicAdd(&acc[(cl[e] & (kSteClasses - 1)) * kSlots], ds);
           }
         }
       }
     }
-    __syncthreads();   // stage par is rewritten two tiles later; keep it simple
+    wait_copies();
+    __syncthreads();
   }
   if (active && valid && lane < 32) {
     float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)qtok * kSteClasses;
 #pragma unroll
     for (int cc = 0; cc < kSteClasses; ++cc)
-      if (cc < a.ste_classes) dst[cc] = acc[cc];
+      if (cc < a.ste_classes) dst[cc] = acc[cc * kSlots];
   }
 }
 
