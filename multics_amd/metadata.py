@@ -321,6 +321,12 @@ def _progs_per_block(topo: BlockTopology, bm: int) -> int:
     return int(sum(_ceil(int(x), bm) for x in _seg_qlens(topo)))
 
 
+def _item_order(P: int, N: int, B: int):
+    """(stream, block) order of the work items: local hubs, players, global,
+    each over all blocks."""
+    return [(s, b) for s in list(range(P, P + N)) + list(range(P)) + [P + N] for b in range(B)]
+
+
 def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
           tiled: bool = False, rows_per_item: int = ROWS_PER_ITEM) -> BuildResult:
     """Run the two device passes and return device tensors."""
@@ -405,14 +411,13 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     # Consecutive items of one player cover consecutive temporal blocks, whose
     # key windows overlap in all but n frames, so the workgroups an XCD runs
     # together share most of their K/V lines in that XCD's L2; the longest
-    # key lists (local hubs) start first.
-    order = [s for s in range(P, P + N)] + list(range(P)) + [P + N]
+    # key lists (local hubs) start first.  (Block-major orders, which run a
+    # block's hub items beside its player items, measured 4-8 % slower at C2.)
     item_start = np.zeros((B, NS), dtype=np.int64)
     cursor = 0
-    for s in order:
-        for b in range(B):
-            item_start[b, s] = cursor
-            cursor += int(nit[b, s])
+    for s, b in _item_order(P, N, B):
+        item_start[b, s] = cursor
+        cursor += int(nit[b, s])
     n_items = cursor
     kv_idx = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
     kv_mask = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
