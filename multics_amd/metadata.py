@@ -321,6 +321,34 @@ def _progs_per_block(topo: BlockTopology, bm: int) -> int:
     return int(sum(_ceil(int(x), bm) for x in _seg_qlens(topo)))
 
 
+class _Upload:
+    """Small host arrays gathered into one buffer and copied to the device with
+    one transfer (each host->device copy costs ~20 us of latency, and a build
+    has a few dozen arrays).  ``add`` returns nothing; ``flush`` uploads and
+    calls each array's setter with its device address (16-byte aligned)."""
+
+    def __init__(self):
+        self._items = []
+
+    def add(self, arr, dtype, setter):
+        self._items.append((np.ascontiguousarray(arr, dtype=dtype), setter))
+
+    def flush(self, dev) -> torch.Tensor:
+        offs, total = [], 0
+        for a, _ in self._items:
+            offs.append(total)
+            total += -(-max(a.nbytes, 1) // 16) * 16
+        host = np.zeros(max(total, 16), np.uint8)
+        for (a, _), o in zip(self._items, offs):
+            host[o:o + a.nbytes] = a.reshape(-1).view(np.uint8)
+        buf = torch.from_numpy(host).to(dev)
+        base = buf.data_ptr()
+        for (_, setter), o in zip(self._items, offs):
+            setter(base + o)
+        self._items = []
+        return buf
+
+
 def _item_order(P: int, N: int, B: int):
     """(stream, block) order of the work items: local hubs, players, global,
     each over all blocks."""
@@ -366,13 +394,14 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
         "ref_qbase": np.asarray(topo.ref_qbase, np.int32).reshape(B, NS),
         "tile_qbase": np.asarray(topo.tile_qbase, np.int32).reshape(B, NS),
     }
-    dv = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in host.items()}
     t = _capi.HierTopo(P=P, N=N, L=topo.L, KL=topo.KL, KG=topo.KG, n_frames=n,
                        n_block=topo.n_block, local_attn=topo.local_attn, direct=int(topo.direct),
                        no_local=int(topo.no_local), use_membership=int(use_mem), B=B,
                        fa_max=fa_max, fl_max=fl_max, fg_max=fg_max, T_mem=T_mem)
-    for k, v in dv.items():
-        setattr(t, k, v.data_ptr())
+    up = _Upload()
+    for k, v in host.items():
+        up.add(v, v.dtype, lambda ptr, k=k: setattr(t, k, ptr))
+    dv = up.flush(dev)
     if topo.labels is None:
         t.labels = None
     if not use_mem:
@@ -382,25 +411,27 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     n_seg = topo.n_seg
-    seg_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
-    til_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
-    den_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
-    log_c = torch.zeros((B, n_seg), dtype=torch.int32, device=dev)
-    tile_c = torch.zeros((B, NS), dtype=torch.int32, device=dev)
+    # the five count arrays in one buffer: one fill, one readback
+    cnt = torch.zeros(4 * B * n_seg + B * NS, dtype=torch.int32, device=dev)
+    seg_c, til_c, den_c, log_c = (cnt[i * B * n_seg:(i + 1) * B * n_seg] for i in range(4))
+    tile_c = cnt[4 * B * n_seg:]
     counts = _capi.HierMetaCounts(seg_count=seg_c.data_ptr(), tiled_count=til_c.data_ptr(),
                                   dense_count=den_c.data_ptr(), logical_count=log_c.data_ptr(),
                                   tile_count=tile_c.data_ptr())
     _capi.call("hier_meta_count", C.byref(t), C.byref(counts), stream)
-    seg_h, til_h, den_h, log_h, tile_h = (x.cpu().numpy().astype(np.int64)
-                                          for x in (seg_c, til_c, den_c, log_c, tile_c))
+    cnt_h = cnt.cpu().numpy().astype(np.int64)
+    seg_h, til_h, den_h, log_h = (cnt_h[i * B * n_seg:(i + 1) * B * n_seg].reshape(B, n_seg)
+                                  for i in range(4))
+    tile_h = cnt_h[4 * B * n_seg:].reshape(B, NS)
 
     out = _capi.HierMetaOut()
     keep = []
 
-    def dbuf(arr, dtype=torch.int64):
-        x = torch.as_tensor(np.asarray(arr), dtype=dtype).to(dev)
-        keep.append(x)
-        return x
+    # the offset arrays of the output layout, uploaded together before the build
+    up = _Upload()
+
+    def dbuf(arr, dtype, field):
+        up.add(np.asarray(arr), dtype, lambda ptr: setattr(out, field, ptr))
 
     # ---- tile list ----------------------------------------------------------
     tile_off = np.concatenate([[0], np.cumsum(tile_h.reshape(-1))])
@@ -423,8 +454,8 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     kv_mask = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
     blk_and = torch.empty(max(n_keys // TILE_KEYS, 1), dtype=torch.int32, device=dev)
     items = torch.empty((max(n_items, 1), 8), dtype=torch.int32, device=dev)
-    out.tile_kv_off = dbuf(tile_off[:-1]).data_ptr()
-    out.tile_item_off = dbuf(item_start.reshape(-1), torch.int32).data_ptr()
+    dbuf(tile_off[:-1], np.int64, "tile_kv_off")
+    dbuf(item_start.reshape(-1), np.int32, "tile_item_off")
     out.rows_per_item = rows_per_item
     out.tile_kv_idx, out.tile_kv_mask = kv_idx.data_ptr(), kv_mask.data_ptr()
     out.tile_blk_and, out.tile_items = blk_and.data_ptr(), items.data_ptr()
@@ -447,9 +478,9 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
         s_pn = torch.empty_like(s_pq)
         s_ps = torch.empty_like(s_pq)
         out.block_m = bm
-        out.seg_prog_off = dbuf(prog_off[:-1]).data_ptr()
-        out.seg_kv_off = dbuf(kv_off[:-1]).data_ptr()
-        out.seg_max_k = dbuf(maxk, torch.int32).data_ptr()
+        dbuf(prog_off[:-1], np.int64, "seg_prog_off")
+        dbuf(kv_off[:-1], np.int64, "seg_kv_off")
+        dbuf(maxk, np.int32, "seg_max_k")
         out.seg_prog_qbase, out.seg_prog_nq, out.seg_prog_seg = (s_pq.data_ptr(), s_pn.data_ptr(),
                                                                  s_ps.data_ptr())
         out.seg_kv_index, out.seg_kv_count = s_kv.data_ptr(), s_cnt.data_ptr()
@@ -474,9 +505,9 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
         t_pq = torch.empty(max(B * npb, 1), dtype=torch.int32, device=dev)
         t_pn = torch.empty_like(t_pq)
         t_ps = torch.empty_like(t_pq)
-        out.tiled_prog_off = dbuf(prog_off[:-1]).data_ptr()
-        out.tiled_kv_off = dbuf(kv_off[:-1]).data_ptr()
-        out.tiled_max_k = dbuf(maxk, torch.int32).data_ptr()
+        dbuf(prog_off[:-1], np.int64, "tiled_prog_off")
+        dbuf(kv_off[:-1], np.int64, "tiled_kv_off")
+        dbuf(maxk, np.int32, "tiled_max_k")
         out.tiled_prog_qbase, out.tiled_prog_nq, out.tiled_prog_seg = (
             t_pq.data_ptr(), t_pn.data_ptr(), t_ps.data_ptr())
         out.tiled_kv_index, out.tiled_kv_valid = t_kv.data_ptr(), t_va.data_ptr()
@@ -492,6 +523,7 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
                 logical_slots=int(log_h[b].sum()), physical_slots=int(til_h[b].sum()),
                 dense_slots=int(den_h[b].sum())))
 
+    keep.append(up.flush(dev))
     _capi.call("hier_meta_build", C.byref(t), C.byref(out), stream)
 
     ranges = tuple(tuple((int(item_start[b, s]), int(item_start[b, s] + nit[b, s]))
@@ -731,14 +763,20 @@ def _lru_put(cache, key, value, env, default):
 
 
 def _freeze(x):
+    """Hashable cache-key form of a (nested) list / array argument."""
     if x is None:
         return None
-    if isinstance(x, np.ndarray):
-        return (x.shape, x.tobytes())
     if torch.is_tensor(x):
-        a = x.detach().cpu().numpy()
-        return (a.shape, a.tobytes())
-    return tuple(_freeze(v) if isinstance(v, (list, tuple, np.ndarray)) else v for v in x)
+        x = x.detach().cpu().numpy()
+    if not isinstance(x, np.ndarray):
+        try:   # rectangular nested lists: one array, one bytes key
+            a = np.asarray(x)
+        except ValueError:   # ragged
+            a = None
+        if a is None or a.dtype == object:
+            return tuple(_freeze(v) if isinstance(v, (list, tuple, np.ndarray)) else v for v in x)
+        x = a
+    return (x.shape, x.dtype.str, x.tobytes())
 
 
 def _build_metadata(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn, agent_frame_lists,
