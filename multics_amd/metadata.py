@@ -350,9 +350,9 @@ class _Upload:
 
 
 def _item_order(P: int, N: int, B: int):
-    """(stream, block) order of the work items: local hubs, players, global,
+    """(stream, block) order of the work items: local hubs, global, players,
     each over all blocks."""
-    return [(s, b) for s in list(range(P, P + N)) + list(range(P)) + [P + N] for b in range(B)]
+    return [(s, b) for s in list(range(P, P + N)) + [P + N] + list(range(P)) for b in range(B)]
 
 
 def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
@@ -438,12 +438,13 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     n_keys = int(tile_off[-1])
     rows = np.array([[n * _qlen(topo, s) for s in range(NS)] for _ in range(B)], dtype=np.int64)
     nit = -(-rows // rows_per_item)
-    # Work-item order: stream-major (local hubs, players, global), then block.
+    # Work-item order: stream-major (local hubs, global, players), then block.
     # Consecutive items of one player cover consecutive temporal blocks, whose
     # key windows overlap in all but n frames, so the workgroups an XCD runs
     # together share most of their K/V lines in that XCD's L2; the longest
-    # key lists (local hubs) start first.  (Block-major orders, which run a
-    # block's hub items beside its player items, measured 4-8 % slower at C2.)
+    # key lists (local hubs) start first and the short global ones do not end
+    # the launch (1 % at C2).  Block-major orders, which run a block's hub
+    # items beside its player items, measured 4-8 % slower at C2.
     item_start = np.zeros((B, NS), dtype=np.int64)
     cursor = 0
     for s, b in _item_order(P, N, B):
