@@ -12,18 +12,21 @@
 // with the same bf16 rounding points as the reference.  The reference rotates
 // in float64; here the rotation runs in fp32 from fp32 cos/sin tables, so a
 // result can differ from the reference by one bf16 ulp.  The RMS spans all
-// heads (the full model dim), so one workgroup owns whole tokens: dim/CPT
-// threads x CPT channels (CPT = 4 up to dim 3072, else 8).  Camera weights
-// stay in registers, packed, while the workgroup walks kTokens tokens two at a
-// time: one workgroup reduction serves both tokens, each unpacked weight feeds
-// both, and the next two tokens' projections and camera rows are loaded while
-// the current two are computed.  V is copied into the requested layout.
+// heads (the full model dim), so one workgroup owns whole tokens of one
+// projection (q or k): dim/CPT threads x CPT channels (CPT = 4 up to dim 3072,
+// else 8).  Camera weights stay in registers, packed, and the workgroup's
+// camera rows in LDS, while the workgroup walks kTokens tokens two at a time:
+// one workgroup reduction serves both tokens, each packed weight pair feeds
+// both (v_dot2_f32_bf16), and the next two tokens' projections are loaded
+// while the current two are computed.  The q workgroups also copy V into the
+// requested layout.
 #include "hier_common.h"
 
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kTokens = 32;
 
 __device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
@@ -55,11 +58,7 @@ __device__ __forceinline__ void block_sum(float* v, float* red) {
   }
 }
 
-// The inputs of one token that the camera / norm stage needs first (loaded a
-// trip ahead); V and the RoPE tables are loaded at the start of the trip that
-// uses them.
-// CPT channels per thread: 4 for model dims up to 3072 (more waves per CU:
-// the camera weights held per thread halve), 8 up to 4096.
+// CPT channels per thread: 4 for model dims up to 3072, 8 up to 4096.
 template <int CPT>
 struct Chw;
 template <>
@@ -67,63 +66,57 @@ struct Chw<4> { typedef u32x2 type; };
 template <>
 struct Chw<8> { typedef u32x4 type; };
 
-template <int C, int CPT>
-struct TokIn {
-  typename Chw<CPT>::type q4, k4;
-  u32x2 cam[C > 0 ? C / 4 : 1];   // C bf16 = C / 4 pairs of packed words
-};
-
+// blockIdx.y selects the projection: 0 = q (and the V copy), 1 = k.  Keeping
+// the two on separate workgroups halves the camera weights each thread holds,
+// which lets two workgroups share a CU.
 template <int C, int kCPT>
 __global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPrologueArgs a) {
   typedef typename Chw<kCPT>::type chw_t;
-  __shared__ float red[16 * 4];
+  constexpr int CW = C > 0 ? C / 2 : 1;          // packed camera words per token
+  __shared__ float red[16 * 2];
+  __shared__ uint32_t camw[kTokens * CW];        // this workgroup's camera rows
+  const bool is_k = blockIdx.y != 0;
+  const uint16_t* const xin = is_k ? a.kx : a.qx;
+  uint16_t* const out = is_k ? a.k_out : a.q_out;
+  const bool copy_v = !is_k && a.v_out != nullptr;
   const int dim = a.H * a.D;
   const int c0 = threadIdx.x * kCPT;        // first channel of this thread
   const int head = c0 / a.D, d0 = c0 - head * a.D;
   const int half = a.D / 2;
   const int m0 = d0 / 2;
+  const int s_begin = blockIdx.x * kTokens;
+  const int s_end = min(a.S, s_begin + kTokens);
 
   // camera weights of this thread's kCPT channels: rows c0.. of [dim][C] are
   // contiguous, loaded as packed bf16 pairs (word i = elements 2i, 2i+1)
   constexpr int NW = C > 0 ? kCPT * C / 8 : 1;     // 16-byte vectors
-  u32x4 wq[NW], wk[NW];
+  u32x4 wc[NW];
   if constexpr (C > 0) {
+    const uint16_t* const w = is_k ? a.w_cam_k : a.w_cam_q;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      wq[i] = *reinterpret_cast<const u32x4*>(a.w_cam_q + (int64_t)c0 * C + 8 * i);
-      wk[i] = *reinterpret_cast<const u32x4*>(a.w_cam_k + (int64_t)c0 * C + 8 * i);
-    }
+    for (int i = 0; i < NW; ++i)
+      wc[i] = *reinterpret_cast<const u32x4*>(w + (int64_t)c0 * C + 8 * i);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.cam + (int64_t)s_begin * C);
+    for (int i = threadIdx.x; i < (s_end - s_begin) * CW; i += blockDim.x) camw[i] = src[i];
   }
-  float gq[kCPT], gk[kCPT];
+  float g[kCPT];
   {
-    const chw_t q4 = *reinterpret_cast<const chw_t*>(a.norm_q_w + c0);
-    const chw_t k4 = *reinterpret_cast<const chw_t*>(a.norm_k_w + c0);
+    const chw_t g4 = *reinterpret_cast<const chw_t*>((is_k ? a.norm_k_w : a.norm_q_w) + c0);
 #pragma unroll
     for (int e = 0; e < kCPT / 2; ++e) {
-      gq[2 * e] = bf2f(q4[e] & 0xffffu); gq[2 * e + 1] = bf2f(q4[e] >> 16);
-      gk[2 * e] = bf2f(k4[e] & 0xffffu); gk[2 * e + 1] = bf2f(k4[e] >> 16);
+      g[2 * e] = bf2f(g4[e] & 0xffffu);
+      g[2 * e + 1] = bf2f(g4[e] >> 16);
     }
   }
-  auto load = [&](int s) {
-    TokIn<C, kCPT> x;
-    x.q4 = *reinterpret_cast<const chw_t*>(a.qx + (int64_t)s * dim + c0);
-    x.k4 = *reinterpret_cast<const chw_t*>(a.kx + (int64_t)s * dim + c0);
-    if constexpr (C > 0) {
-#pragma unroll
-      for (int i = 0; i < C / 4; ++i)
-        x.cam[i] = *reinterpret_cast<const u32x2*>(a.cam + (int64_t)s * C + 4 * i);
-    }
-    return x;
-  };
+  auto load = [&](int s) { return *reinterpret_cast<const chw_t*>(xin + (int64_t)s * dim + c0); };
+  if constexpr (C > 0) __syncthreads();   // camera rows staged
 
-  // Two tokens per trip (one reduction for both, each unpacked camera weight
-  // feeds both), the next two tokens' inputs loaded during the current ones.
-  // An odd last token is paired with itself and stored once.
-  const int s_begin = blockIdx.x * kTokens;
-  const int s_end = min(a.S, s_begin + kTokens);
-  TokIn<C, kCPT> n0 = load(s_begin), n1 = load(min(s_begin + 1, s_end - 1));
+  // Two tokens per trip (one reduction for both, each packed camera weight pair
+  // feeds both), the next two tokens' projections loaded during the current
+  // ones.  An odd last token is paired with itself and stored once.
+  chw_t n0 = load(s_begin), n1 = load(min(s_begin + 1, s_end - 1));
   for (int s = s_begin; s < s_end; s += 2) {
-    const TokIn<C, kCPT> x[2] = {n0, n1};
+    const chw_t x[2] = {n0, n1};
     const bool second = s + 1 < s_end;
     const int s1 = second ? s + 1 : s;
     typedef float rope_t __attribute__((ext_vector_type(kCPT / 2)));
@@ -133,7 +126,7 @@ __global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPro
     sn[0] = *reinterpret_cast<const rope_t*>(a.rope_sin + (int64_t)s * half + m0);
     cs[1] = *reinterpret_cast<const rope_t*>(a.rope_cos + (int64_t)s1 * half + m0);
     sn[1] = *reinterpret_cast<const rope_t*>(a.rope_sin + (int64_t)s1 * half + m0);
-    if (a.v_out) {
+    if (copy_v) {
       v4[0] = *reinterpret_cast<const chw_t*>(a.vx + (int64_t)s * dim + c0);
       v4[1] = *reinterpret_cast<const chw_t*>(a.vx + (int64_t)s1 * dim + c0);
     }
@@ -141,91 +134,64 @@ __global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPro
       n0 = load(s + 2);
       n1 = load(min(s + 3, s_end - 1));
     }
-    float q[2][kCPT], k[2][kCPT];
+    float q[2][kCPT];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < kCPT / 2; ++e) {
-        q[t][2 * e] = bf2f(x[t].q4[e] & 0xffffu); q[t][2 * e + 1] = bf2f(x[t].q4[e] >> 16);
-        k[t][2 * e] = bf2f(x[t].k4[e] & 0xffffu); k[t][2 * e + 1] = bf2f(x[t].k4[e] >> 16);
+        q[t][2 * e] = bf2f(x[t][e] & 0xffffu);
+        q[t][2 * e + 1] = bf2f(x[t][e] >> 16);
       }
     if constexpr (C > 0) {
-      // keep the weights packed: stops the unpack being hoisted out of the
-      // token loop (it would need 2*8*C fp32 registers)
-#pragma unroll
-      for (int i = 0; i < NW; ++i) {
-        asm volatile("" : "+v"(wq[i]));
-        asm volatile("" : "+v"(wk[i]));
-      }
-      float cam[2][C];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < C / 4; ++i)
-#pragma unroll
-          for (int w = 0; w < 2; ++w) {
-            cam[t][4 * i + 2 * w] = bf2f(x[t].cam[i][w] & 0xffffu);
-            cam[t][4 * i + 2 * w + 1] = bf2f(x[t].cam[i][w] >> 16);
-          }
+      // packed bf16 pairs straight into v_dot2_f32_bf16: weight word w holds
+      // elements (e, 2c), (e, 2c+1), camera word c holds cam[2c], cam[2c+1];
+      // the products are exact in fp32 and accumulate in c order
+      const uint32_t* cr[2] = {camw + (s - s_begin) * CW, camw + (s1 - s_begin) * CW};
 #pragma unroll
       for (int e = 0; e < kCPT; ++e) {
-        float aq[2] = {0.f, 0.f}, ak[2] = {0.f, 0.f};
+        float acc[2] = {0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < C / 2; ++c) {
-          const int w = (e * C) / 2 + c;     // packed word of elements (e, 2c), (e, 2c+1)
-          const uint32_t xq = wq[w >> 2][w & 3], xk = wk[w >> 2][w & 3];
-          const float wq0 = __uint_as_float(xq << 16), wq1 = __uint_as_float(xq & 0xffff0000u);
-          const float wk0 = __uint_as_float(xk << 16), wk1 = __uint_as_float(xk & 0xffff0000u);
+        for (int c = 0; c < CW; ++c) {
+          const int w = e * CW + c;
+          // (through a scalar temporary: a bit-cast applied to a vector
+          // element subscript directly reads element 0)
+          const uint32_t uw = wc[w >> 2][w & 3];
+          const bf16x2 xw = __builtin_bit_cast(bf16x2, uw);
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            aq[t] = fmaf(cam[t][2 * c], wq0, aq[t]);
-            aq[t] = fmaf(cam[t][2 * c + 1], wq1, aq[t]);
-            ak[t] = fmaf(cam[t][2 * c], wk0, ak[t]);
-            ak[t] = fmaf(cam[t][2 * c + 1], wk1, ak[t]);
+            const uint32_t uc = cr[t][c];
+            acc[t] = __builtin_amdgcn_fdot2_f32_bf16(xw, __builtin_bit_cast(bf16x2, uc), acc[t],
+                                                     false);
           }
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          q[t][e] = rbf(q[t][e] + rbf(aq[t]));
-          k[t][e] = rbf(k[t][e] + rbf(ak[t]));
-        }
+        for (int t = 0; t < 2; ++t) q[t][e] = rbf(q[t][e] + rbf(acc[t]));
       }
     }
-    float ss[4] = {0.f, 0.f, 0.f, 0.f};
+    float ss[2] = {0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < kCPT; ++e) {
-        ss[2 * t] = fmaf(q[t][e], q[t][e], ss[2 * t]);
-        ss[2 * t + 1] = fmaf(k[t][e], k[t][e], ss[2 * t + 1]);
-      }
-    block_sum<4>(ss, red);
+      for (int e = 0; e < kCPT; ++e) ss[t] = fmaf(q[t][e], q[t][e], ss[t]);
+    block_sum<2>(ss, red);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (t == 1 && !second) break;
-      const float iq = rsqrtf(ss[2 * t] / (float)dim + a.eps);
-      const float ik = rsqrtf(ss[2 * t + 1] / (float)dim + a.eps);
+      const float inv = rsqrtf(ss[t] / (float)dim + a.eps);
 #pragma unroll
-      for (int e = 0; e < kCPT; ++e) {
-        q[t][e] = rbf(rbf(q[t][e] * iq) * gq[e]);
-        k[t][e] = rbf(rbf(k[t][e] * ik) * gk[e]);
-      }
+      for (int e = 0; e < kCPT; ++e) q[t][e] = rbf(rbf(q[t][e] * inv) * g[e]);
       // RoPE on (even, odd) channel pairs of this head
-      chw_t qv, kv;
+      chw_t qv;
 #pragma unroll
       for (int e = 0; e < kCPT / 2; ++e) {
         const float c = cs[t][e], sv = sn[t][e];
         const float qr = q[t][2 * e] * c - q[t][2 * e + 1] * sv;
         const float qi = q[t][2 * e] * sv + q[t][2 * e + 1] * c;
-        const float kr = k[t][2 * e] * c - k[t][2 * e + 1] * sv;
-        const float ki = k[t][2 * e] * sv + k[t][2 * e + 1] * c;
         qv[e] = f2bf(qr) | (f2bf(qi) << 16);
-        kv[e] = f2bf(kr) | (f2bf(ki) << 16);
       }
       const int64_t off = (int64_t)(s + t) * a.out_stride_s + (int64_t)head * a.out_stride_h + d0;
-      *reinterpret_cast<chw_t*>(a.q_out + off) = qv;
-      *reinterpret_cast<chw_t*>(a.k_out + off) = kv;
-      if (a.v_out) *reinterpret_cast<chw_t*>(a.v_out + off) = v4[t];
+      *reinterpret_cast<chw_t*>(out + off) = qv;
+      if (copy_v) *reinterpret_cast<chw_t*>(a.v_out + off) = v4[t];
     }
   }
 }
@@ -263,11 +229,11 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   const int threads = nthr;
   const hipStream_t st = (hipStream_t)stream;
   if (kCPT == 4) {
-    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 4>), dim3(grid), dim3(threads), 0, st, a);
-    else hipLaunchKernelGGL((prologue_kernel<0, 4>), dim3(grid), dim3(threads), 0, st, a);
+    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 4>), dim3(grid, 2), dim3(threads), 0, st, a);
+    else hipLaunchKernelGGL((prologue_kernel<0, 4>), dim3(grid, 2), dim3(threads), 0, st, a);
   } else {
-    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 8>), dim3(grid), dim3(threads), 0, st, a);
-    else hipLaunchKernelGGL((prologue_kernel<0, 8>), dim3(grid), dim3(threads), 0, st, a);
+    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 8>), dim3(grid, 2), dim3(threads), 0, st, a);
+    else hipLaunchKernelGGL((prologue_kernel<0, 8>), dim3(grid, 2), dim3(threads), 0, st, a);
   }
   return hier::check_launch("prologue_kernel");
 }
