@@ -129,28 +129,34 @@ struct QCtx {
   uint32_t bits;
 };
 
-// Tile t: copies tile t+1 into stage PAR^1 and loads the key indices and the
-// visibility flags of tile t+1 (blk: flags of tile t on entry, of t+1 on
-// exit), then works on stage PAR.  Every global load is waited for with the
-// copies at the end, so nothing in the MFMA work waits on the copies in flight.
+// Tile t: works on stage PAR while tile t+1 is copied into stage PAR^1 in two
+// bursts, K (with the masks) before the first 32-key block and V before the
+// second, and loads the key indices and the visibility flags of tile t+1
+// (blk: flags of tile t on entry, of t+1 on exit).  Every global load is
+// waited for with the copies at the end, so nothing in the MFMA work waits on
+// the copies in flight.
 template <int D, int PAR>
 __device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, uint32_t& blk,
                                         const QStages& st) {
   uint32_t blk_next = 0;
-  if (t + 1 < c.nt) {
+  const bool more = t + 1 < c.nt;
+  if (more) {
     copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, st.k[PAR ^ 1], c.wave);
-    copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, inext, st.v[PAR ^ 1], c.wave);
     copy_dwords(c.kv_mask + (t + 1) * kSlab, st.m[PAR ^ 1], c.lane);
-    inext = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
     blk_next = c.blk[t + 1];
   }
-  if (c.active) {
+  {
     const char* ks = st.k[PAR];
     const char* vs = st.v[PAR];
     const uint32_t* mk = reinterpret_cast<const uint32_t*>(st.m[PAR]);
     const bool need = (blk & c.bits) != c.bits;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
+      if (kb == 1 && more) {
+        copy_tile<D, kRowRead>(c.gv, c.v_ss_b, c.cv, inext, st.v[PAR ^ 1], c.wave);
+        inext = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+      }
+      if (!c.active) continue;
       const f32x16 s = row_mfma<D>(c.q, ks, c.krow, kb);
       const f32x16 dp = row_mfma<D>(c.dov, vs, c.vrow, kb);
       bf16x8 dsb[2];
@@ -319,16 +325,20 @@ __device__ __forceinline__ void kdv_copy(KCtx<D>& c, int t, const Idx<D>& ix, in
   if constexpr (PASS == kPassDK) dma4_lane(c.delta + qtok, stage_w + 2 * Geo<D>::MBYTES);
 }
 
+// Query tile t of a key item: works on stage PAR while tile t+1 is copied into
+// stage PAR^1 in two bursts, Q (with the masks and the per-row lse / delta)
+// before the first 32-query block and dO before the second.
 template <int D, int PASS, int PAR>
 __device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int& qnext,
                                           const KStages& st) {
-  if (t + 1 < c.nt) {
-    kdv_copy<D, PASS>(c, t + 1, inext, qnext, st.q[PAR ^ 1], st.d[PAR ^ 1], st.w[PAR ^ 1]);
-    const int tn = min(t + 2, c.nt - 1);
-    inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
-    qnext = c.q_idx[tn * kSlab + c.lane];
+  const bool more = t + 1 < c.nt;
+  if (more) {
+    copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, inext, st.q[PAR ^ 1], c.wave);
+    copy_dwords(c.q_mask + (t + 1) * kSlab, st.w[PAR ^ 1], c.lane);
+    dma4_lane(c.lse2 + qnext, st.w[PAR ^ 1] + Geo<D>::MBYTES);
+    if constexpr (PASS == kPassDK) dma4_lane(c.delta + qnext, st.w[PAR ^ 1] + 2 * Geo<D>::MBYTES);
   }
-  if (c.active) {
+  {
     const char* qs = st.q[PAR];
     const char* ds_ = st.d[PAR];
     const char* ws = st.w[PAR];
@@ -337,6 +347,13 @@ __device__ __forceinline__ void dkdv_tile(KCtx<D>& c, int t, Idx<D>& inext, int&
     const float* dl = reinterpret_cast<const float*>(ws + 2 * Geo<D>::MBYTES);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
+      if (qb == 1 && more) {
+        copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, inext, st.d[PAR ^ 1], c.wave);
+        const int tn = min(t + 2, c.nt - 1);
+        inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
+        qnext = c.q_idx[tn * kSlab + c.lane];
+      }
+      if (!c.active) continue;
       const f32x16 s = row_mfma<D>(c.kt, qs, c.row, qb);
       f32x16 dp;
       if constexpr (PASS == kPassDK) dp = row_mfma<D>(c.vt, ds_, c.row, qb);
