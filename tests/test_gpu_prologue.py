@@ -20,12 +20,21 @@ def _freqs(P, T, h, w, KG_total):
 
 @pytest.mark.parametrize("camera", [False, True])
 @pytest.mark.parametrize("layout", ["shd", "hsd"])
-def test_prologue_matches_oracle(camera, layout):
+@pytest.mark.parametrize("shape", ["small", "odd_tokens", "dim4096"])
+def test_prologue_matches_oracle(camera, layout, shape):
+    """small: 168 tokens, dim 512 (4 channels per thread); odd_tokens: 141
+    tokens, so the last workgroup ends on a token paired with itself;
+    dim4096: 32 heads, 8 channels per thread."""
     need_gpu()
-    say("prologue camera", camera, layout)
+    say("prologue camera", camera, layout, shape)
     P, T, h, w, H, D = 2, 3, 4, 5, 4, 128
     K_total = 2 * 5 + 6
+    if shape == "odd_tokens":
+        h, w, K_total = 3, 5, 2 * 5 + 7
+    elif shape == "dim4096":
+        T, H = 2, 32
     S = P * T * h * w + T * K_total
+    assert shape != "odd_tokens" or S % 2 == 1
     dim = H * D
     g = torch.Generator().manual_seed(5)
     qx = (torch.randn(S, dim, generator=g) * 0.7).to(torch.bfloat16)
