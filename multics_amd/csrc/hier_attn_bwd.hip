@@ -522,6 +522,90 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
 #pragma unroll
     for (int cc = 0; cc < kSteClasses; ++cc) acc[cc * kSlots] = 0.f;
 
+  if (row_count <= 32) {
+    // At most 32 rows (a hub slot's rows against long key lists): the four
+    // waves share the rows and split the 32-key blocks (wave w takes blocks w,
+    // w + 4, ...), reading K and V rows straight into the MFMA operand
+    // registers, so the loop has no LDS stages and no barriers.  Each wave
+    // sums into its own slots; the four are added in wave order at the end.
+    const int r = lane & 31;
+    const bool valid = r < row_count;
+    const int ri = row_start + (valid ? r : 0);
+    const int qframe = ri / qlen;
+    const int qtok = qbase + qframe * qstride + (ri - qframe * qlen);
+    bf16x8 q[Geo<D>::NC], dov[Geo<D>::NC];
+    load_row<D>(q, a.q + (int64_t)qtok * a.q_ss + (int64_t)head * a.q_sh, lane);
+    load_row<D>(dov, a.dout + (int64_t)qtok * a.do_ss + (int64_t)head * a.do_sh, lane);
+    const int64_t srow = (int64_t)head * a.lse_stride_h + qtok;
+    const float lse2 = a.lse2[srow], delta = a.delta[srow];
+    const int nb = kv_cnt / 32;
+    for (int j = wave; j < nb; j += kWaves) {
+      const int64_t key = kv_idx[32 * j + r];
+      // operand layout of row_mfma: lane l holds elements 16c + 8(l/32) .. +8
+      // of key row 32j + l%32 in its k-step c
+      const char* kp = gk + key * k_ss_b + 16 * (lane >> 5);
+      const char* vp = gv + key * v_ss_b + 16 * (lane >> 5);
+      bf16x8 ka[Geo<D>::NC], va[Geo<D>::NC];
+#pragma unroll
+      for (int c = 0; c < Geo<D>::NC; ++c) {
+        ka[c] = *reinterpret_cast<const bf16x8*>(kp + 32 * c);
+        va[c] = *reinterpret_cast<const bf16x8*>(vp + 32 * c);
+      }
+      const f32x16 zero = {};
+      f32x16 s = mfma(ka[0], q[0], zero), dp = mfma(va[0], dov[0], zero);
+#pragma unroll
+      for (int c = 1; c < Geo<D>::NC; ++c) {
+        s = mfma(ka[c], q[c], s);
+        dp = mfma(va[c], dov[c], dp);
+      }
+      // The keys of a block mostly share one class (a player's frame run):
+      // a lane whose 16 keys do adds their sum once, otherwise each term.
+      float ds[16];
+      uint32_t cls[16];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int k0 = 32 * j + 8 * g4 + 4 * (lane >> 5);
+        const u32x4 w = *reinterpret_cast<const u32x4*>(&kv_mask[k0]);
+        const u32x4 cl = *reinterpret_cast<const u32x4*>(&kv_cls[k0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g4 + e;
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[i], c2, -lse2));
+          ds[i] = __uint_as_float(__float_as_uint(p * (dp[i] - delta)) & keep_mask(w[e], qframe));
+          cls[i] = cl[e] & (kSteClasses - 1);
+        }
+      }
+      bool same = true;
+#pragma unroll
+      for (int i = 1; i < 16; ++i) same = same && cls[i] == cls[0];
+      if (valid) {
+        if (same) {
+          float t = ds[0];
+#pragma unroll
+          for (int i = 1; i < 16; ++i) t += ds[i];
+          atomicAdd(&acc[cls[0] * kSlots], t);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) atomicAdd(&acc[cls[i] * kSlots], ds[i]);
+        }
+      }
+    }
+    __syncthreads();
+    if (wave == 0 && valid && lane < 32) {
+      const float* sum = reinterpret_cast<const float*>(lds + SLds<D>::AOFF) + lane;
+      float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)qtok * kSteClasses;
+#pragma unroll
+      for (int cc = 0; cc < kSteClasses; ++cc)
+        if (cc < a.ste_classes) {
+          float t = sum[cc * kSlots];
+#pragma unroll
+          for (int w = 1; w < kWaves; ++w) t += sum[cc * kSlots + 32 * w];
+          dst[cc] = t;
+        }
+    }
+    return;
+  }
+
   const int r = wave * 32 + (lane & 31);
   const bool valid = r < row_count;
   const int ri = row_start + (valid ? r : 0);
