@@ -23,11 +23,10 @@ hier_tiled_attention.py:165-179).
 from __future__ import annotations
 
 import ctypes as C
-import math
 import os
 from collections import OrderedDict
 from dataclasses import dataclass, field
-from typing import Optional, Sequence
+from typing import Optional
 
 import numpy as np
 import torch

@@ -28,8 +28,6 @@ autograd, the fused HIP prologue (camera + RMSNorm + gain + RoPE in one pass).
 
 from __future__ import annotations
 
-import math
-from typing import Optional
 
 import torch
 import torch.nn as nn

@@ -14,7 +14,7 @@ multics/models/wan_video_dit.py:338-389): per token 64 rotations in four bands
 from __future__ import annotations
 
 import os
-from typing import Sequence, Tuple
+from typing import Tuple
 
 import torch
 
