@@ -7,6 +7,9 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
   rows written as 0 (hier_segmented_attention.py:104-109,
   hier_tiled_attention.py:432-459).  Evaluated one row block at a time from
   ``oracle.masks.mask_rows`` so C2-sized rows never need an S x S matrix.
+* ``attention_grads_at`` -- dQ at chosen query rows and dK / dV at chosen key
+  rows of ``masked_attention`` (the SDPA backward: dS = P (dP - delta)),
+  for bench-size sequences where autograd over every row is too large.
 * ``rms_norm``, ``camera_qk``, ``rope_apply``, ``project_qk`` -- the Q/K
   prologue (attention.py:231-242, 307-320, 355-365; rope.py:248-254) with the
   reference's bf16 rounding points; RoPE in float64 as the reference does.
@@ -18,7 +21,8 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 Parity pins: masked attention is the textbook softmax(QK^T/sqrt(D)) V with the
 dense mask of ``oracle.masks`` (itself pinned against the reference's tests and
 golden layouts), cross-checked against an independent per-row numpy loop on
-small shapes; RMSNorm/RoPE/freqs against closed forms and the simplex
+small shapes; ``attention_grads_at`` against torch autograd through
+``masked_attention`` on small shapes; RMSNorm/RoPE/freqs against closed forms and the simplex
 invariants of tests/test_simplex_rope.py:21-54; camera12 against the rigid
 transform identities (anchor frame maps to the identity pose).
 """
@@ -64,6 +68,55 @@ def masked_attention(q, k, v, topo: FullTopology, *, rows=None, row_block: int =
         o = torch.einsum("hqk,khd->qhd", p, vf)
         out[r0:r0 + len(rr)] = o * live[:, None, None]
     return out
+
+
+def attention_grads_at(q, k, v, dout, topo: FullTopology, *, q_rows, k_rows, scale=None,
+                       row_block: int = 2048):
+    """Gradients of ``sum(masked_attention(q, k, v) * dout)``: dQ at ``q_rows``
+    and dK, dV at ``k_rows`` ([n, H, D] fp32 each).
+
+    Per query row i with visible keys j: P_ij = softmax_j(scale q_i.k_j),
+    O_i = sum_j P_ij v_j, delta_i = dO_i.O_i, dS_ij = P_ij (dO_i.v_j - delta_i);
+    dQ_i = scale sum_j dS_ij k_j, dK_j = scale sum_i dS_ij q_i and
+    dV_j = sum_i P_ij dO_i.  Inactive local-hub rows output 0, so their dO
+    counts as 0.  dK / dV need every row that sees a chosen key, so all rows
+    are visited, ``row_block`` at a time (memory O(row_block x S)).
+    """
+    S, H, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    qf, kf, vf, df = (t.float() for t in (q, k, v, dout))
+    df = df * torch.from_numpy(~inactive_local_rows(topo))[:, None, None]
+    q_rows = np.ascontiguousarray(q_rows, dtype=np.int64)
+    k_rows = np.ascontiguousarray(k_rows, dtype=np.int64)
+    q_pos = {int(r): i for i, r in enumerate(q_rows)}
+    kr = torch.from_numpy(k_rows)
+    dq = torch.zeros((len(q_rows), H, D))
+    dk = torch.zeros((len(k_rows), H, D))
+    dv = torch.zeros((len(k_rows), H, D))
+    for r0 in range(0, S, row_block):
+        rr = np.arange(r0, min(S, r0 + row_block))
+        rt = torch.from_numpy(rr)
+        m = torch.from_numpy(mask_rows(topo, q_idx=rr))                     # [b, S]
+        s = torch.einsum("qhd,khd->hqk", qf[rt], kf) * scale
+        s = s.masked_fill(~m[None], float("-inf"))
+        p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)             # [H, b, S]
+        o = torch.einsum("hqk,khd->qhd", p, vf)
+        delta = (df[rt] * o).sum(-1)                                        # [b, H]
+        # dK, dV at the chosen keys
+        dp_k = torch.einsum("qhd,khd->hqk", df[rt], vf[kr])                 # [H, b, nk]
+        p_k = p[:, :, kr]
+        ds_k = p_k * (dp_k - delta.T[:, :, None])
+        dk += torch.einsum("hqk,qhd->khd", ds_k, qf[rt]) * scale
+        dv += torch.einsum("hqk,qhd->khd", p_k, df[rt])
+        # dQ at the chosen rows of this block
+        sel = [i for i, r in enumerate(rr) if int(r) in q_pos]
+        if sel:
+            si = torch.tensor(sel)
+            dp = torch.einsum("qhd,khd->hqk", df[rt[si]], vf)
+            ds = p[:, si] * (dp - delta[si].T[:, :, None])
+            g = torch.einsum("hqk,khd->qhd", ds, kf) * scale
+            dq[torch.tensor([q_pos[int(rr[i])] for i in sel])] = g
+    return dq, dk, dv
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:

@@ -1,0 +1,114 @@
+"""Parity at the full sizes of the bench configurations, on sampled rows.
+
+An output row depends only on its query, the keys and values it sees and its
+mask row, so a sample of rows is checked exactly against the oracle at sizes
+where an S x S oracle pass per head would not fit a test.  The sample holds
+every stream kind (players, local hubs, global hubs) of the first, middle and
+last temporal blocks, the first and last rows of each player block (a block's
+last 128-row work item holds its 20 remaining rows) and random rows.  The
+backward at C5 takes dQ at the sampled rows and dK / dV at the same key rows
+from ``oracle.attention.attention_grads_at``.  Tolerances as in the small
+cases: forward max-abs 2e-2 / mean-abs 2e-3, log-sum-exp within 2^-8;
+gradients within 2 % of the reference's max and 1 % of its mean.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from multics_amd import metadata as M
+from multics_amd.kernels import hier_attention, hier_attention_forward
+from oracle.attention import attention_grads_at, masked_attention
+from oracle.masks import FullTopology, inactive_local_rows, mask_rows
+from tests.gpu_util import err_stats, need_gpu, say
+from tests.test_gpu_backward import _check
+
+pytestmark = pytest.mark.gpu
+MAX_ABS, MEAN_ABS = 2e-2, 2e-3
+
+
+def _case(cfg):
+    """The bench's topology of ``cfg`` for the HIP builder and the oracle."""
+    P, T, L, N, KL, KG, n, W, _, D, grp = bench.CONFIGS[cfg]
+    first, mem, go = bench.grouping(grp, P, T, N, np.random.default_rng(bench.SEED))
+    labels = None if grp == "logits" else first
+    meta = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W, direct=True,
+                                    labels=labels, membership=mem, global_only=go)
+    if mem is None:
+        topo = FullTopology(P, T, L, N, KL, KG, n, W, True, labels=labels)
+    else:
+        topo = FullTopology(P, T, L, N, KL, KG, n, W, True, membership=mem, global_only=go)
+    return meta, topo, D
+
+
+def _rows(topo, rng, n_random=64):
+    P, T, L, N, KL, KG, n = topo.P, topo.T, topo.L, topo.N, topo.KL, topo.KG, topo.n
+    a0, g0 = P * T * L, P * T * L + T * N * KL
+    nb = -(-T // n)
+    rows = set(rng.choice(topo.S, n_random, replace=False).tolist())
+    for b in sorted({0, nb // 2, nb - 1}):
+        f0, f1 = b * n, min(T, b * n + n)
+        for p in range(P):
+            base, cnt = p * T * L + f0 * L, (f1 - f0) * L
+            rows |= {base, base + 127, base + 128, base + cnt - 21, base + cnt - 1}
+        rows |= set(range(a0 + f0 * N * KL, a0 + f1 * N * KL))
+        rows |= set(range(g0 + f0 * KG, g0 + f1 * KG))
+    return np.array(sorted(r for r in rows if 0 <= r < topo.S), dtype=np.int64)
+
+
+def _inputs(S, H, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [(torch.randn(S, H, D, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3)]
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c3", "p10"])
+def test_forward_full_size_sampled_rows(cfg):
+    need_gpu()
+    meta, topo, D = _case(cfg)
+    H = 4
+    say("full-size forward", cfg, "S", topo.S)
+    tiles = M.build(meta, "cuda").tiles
+    q, k, v = _inputs(topo.S, H, D, seed=21)
+    out = torch.zeros(topo.S, H, D, dtype=torch.bfloat16, device="cuda")
+    lse = torch.full((H, topo.S), float("nan"), dtype=torch.float32, device="cuda")
+    hier_attention_forward(q.cuda(), k.cuda(), v.cuda(), tiles, out, lse=lse)
+    torch.cuda.synchronize()
+    rows = _rows(topo, np.random.default_rng(5))
+    rt = torch.from_numpy(rows)
+    say(f"  {len(rows)} sampled rows")
+    ref = masked_attention(q, k, v, topo, rows=rows)
+    got = out.cpu()[rt]
+    mx, mn = err_stats(got, ref)
+    say(f"  max-abs {mx:.3e} mean-abs {mn:.3e}")
+    assert torch.isfinite(got.float()).all()
+    assert mx <= MAX_ABS and mn <= MEAN_ABS
+    m = torch.from_numpy(mask_rows(topo, q_idx=rows))
+    s = torch.einsum("qhd,khd->hqk", q[rt].float(), k.float()) / math.sqrt(D)
+    ref_lse = torch.logsumexp(s.masked_fill(~m[None], float("-inf")), dim=-1)
+    live = torch.from_numpy(~inactive_local_rows(topo)[rows])
+    got_lse = lse.cpu()[:, rt]
+    assert torch.isneginf(got_lse[:, ~live]).all()
+    assert (got_lse[:, live] - ref_lse[:, live]).abs().max() < 2.0 ** -8
+
+
+def test_backward_full_size_sampled_rows():
+    need_gpu()
+    meta, topo, D = _case("c5")
+    H = 2
+    say("full-size backward c5 S", topo.S)
+    tiles = M.build(meta, "cuda").tiles
+    q, k, v = _inputs(topo.S, H, D, seed=23)
+    dout = torch.randn(topo.S, H, D, generator=torch.Generator().manual_seed(24)).to(torch.bfloat16)
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    hier_attention(qd, kd, vd, tiles).backward(dout.cuda())
+    torch.cuda.synchronize()
+    rows = _rows(topo, np.random.default_rng(6))
+    rt = torch.from_numpy(rows)
+    say(f"  {len(rows)} sampled rows")
+    dq, dk, dv = attention_grads_at(q, k, v, dout, topo, q_rows=rows, k_rows=rows)
+    _check("dq", qd.grad.cpu()[rt], dq)
+    _check("dk", kd.grad.cpu()[rt], dk)
+    _check("dv", vd.grad.cpu()[rt], dv)
