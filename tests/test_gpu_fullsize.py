@@ -7,7 +7,9 @@ every stream kind (players, local hubs, global hubs) of the first, middle and
 last temporal blocks, the first and last rows of each player block (a block's
 last 128-row work item holds its 20 remaining rows) and random rows.  The
 backward at C5 takes dQ at the sampled rows and dK / dV at the same key rows
-from ``oracle.attention.attention_grads_at``.  Tolerances as in the small
+from ``oracle.attention.attention_grads_at``; the C4 rollout (paged KV cache,
+window full) compares sampled rows of its last blocks with the full-sequence
+oracle, which an in-order rollout equals.  Tolerances as in the small
 cases: forward max-abs 2e-2 / mean-abs 2e-3, log-sum-exp within 2^-8;
 gradients within 2 % of the reference's max and 1 % of its mean.
 """
@@ -21,6 +23,7 @@ import torch
 import bench
 from multics_amd import metadata as M
 from multics_amd.kernels import hier_attention, hier_attention_forward
+from multics_amd.paged_cache import HierPagedKVCache
 from oracle.attention import attention_grads_at, masked_attention
 from oracle.masks import FullTopology, inactive_local_rows, mask_rows
 from tests.gpu_util import err_stats, need_gpu, say
@@ -112,3 +115,53 @@ def test_backward_full_size_sampled_rows():
     _check("dq", qd.grad.cpu()[rt], dq)
     _check("dk", kd.grad.cpu()[rt], dk)
     _check("dv", vd.grad.cpu()[rt], dv)
+
+
+def _block_rows(topo, b):
+    """Full-sequence rows of temporal block b in the block's own token order
+    (players, then local hubs, then global hubs, each frame-major)."""
+    P, T, L, N, KL, KG, n = topo.P, topo.T, topo.L, topo.N, topo.KL, topo.KG, topo.n
+    f = np.arange(b * n, min(T, b * n + n))
+    a0, g0 = P * T * L, P * T * L + T * N * KL
+    players = [p * T * L + (f[:, None] * L + np.arange(L)[None]).ravel() for p in range(P)]
+    local = (a0 + f[:, None] * N * KL + np.arange(N * KL)[None]).ravel()
+    glob = (g0 + f[:, None] * KG + np.arange(KG)[None]).ravel()
+    return np.concatenate(players + [local, glob]).astype(np.int64)
+
+
+def test_rollout_full_size_sampled_rows():
+    need_gpu()
+    P, T, L, N, KL, KG, n, W, _, D, grp = bench.CONFIGS["c4"]
+    H = 2
+    _, mem, go = bench.grouping(grp, P, T, N, np.random.default_rng(bench.SEED))
+    topo = FullTopology(P, T, L, N, KL, KG, n, W, True, membership=mem, global_only=go)
+    act = mem.any(-1)
+    say("full-size rollout c4 S", topo.S)
+    q, k, v = _inputs(topo.S, H, D, seed=25)
+    cache = HierPagedKVCache(num_players=P, num_groups=N, num_patches=L, num_local_hub_tokens=KL,
+                             num_global_hub_tokens=KG, num_heads=H, head_dim=D, local_attn_size=W,
+                             num_frame_per_block=n, device="cuda")
+    rng = np.random.default_rng(7)
+    nb = T // n
+    for b in range(nb):
+        rows = _block_rows(topo, b)
+        rt = torch.from_numpy(rows)
+        cache.append(k[rt].cuda(), v[rt].cuda(), b * n, n, act[b * n:b * n + n])
+        if b < nb - 2:
+            continue
+        frames, bases, lact = cache.window(b * n + n - 1)
+        tiles = M.cached_tiles(device="cuda", P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=n,
+                               local_attn=W, frames=frames, tile_bases=bases,
+                               local_active_frames=lact, labels=None,
+                               q_active=act[b * n:b * n + n].tolist(), direct_player=True,
+                               membership=mem, global_only=go)
+        out = torch.zeros(len(rows), H, D, dtype=torch.bfloat16, device="cuda")
+        hier_attention_forward(q[rt].cuda(), cache.k, cache.v, tiles, out)
+        torch.cuda.synchronize()
+        loc = np.unique(np.concatenate([rng.choice(len(rows), 96, replace=False),
+                                        np.arange(P) * n * L, np.arange(P) * n * L + n * L - 1,
+                                        np.arange(P * n * L, len(rows))]))
+        ref = masked_attention(q, k, v, topo, rows=rows[loc])
+        mx, mn = err_stats(out.cpu()[torch.from_numpy(loc)], ref)
+        say(f"  block {b}: {len(loc)} sampled rows, max-abs {mx:.3e} mean-abs {mn:.3e}")
+        assert mx <= MAX_ABS and mn <= MEAN_ABS
