@@ -95,6 +95,26 @@ def test_forward_full_size_sampled_rows(cfg):
     got_lse = lse.cpu()[:, rt]
     assert torch.isneginf(got_lse[:, ~live]).all()
     assert (got_lse[:, live] - ref_lse[:, live]).abs().max() < 2.0 ** -8
+    # the tile list's key set of every sampled row equals its mask row, exactly
+    _check_key_sets(tiles, rows, m.numpy(), ~live.numpy())
+
+
+def _check_key_sets(tiles, rows, m, dead):
+    items = tiles.items[:tiles.n_items].cpu().numpy()
+    idx = tiles.kv_idx.cpu().numpy()
+    msk = tiles.kv_mask.cpu().numpy().view(np.uint32)
+    pos = {int(r): i for i, r in enumerate(rows)}
+    seen = np.zeros(len(rows), dtype=np.int64)
+    for qbase, qstride, qlen, r0, rc, off, cnt, _ in items:
+        j, i = np.divmod(np.arange(r0, r0 + rc), qlen)
+        qs = qbase + j * qstride + i
+        for jj, qq in zip(j[np.isin(qs, rows)], qs[np.isin(qs, rows)]):
+            k = pos[int(qq)]
+            seen[k] += 1
+            got = set(idx[off:off + cnt][((msk[off:off + cnt] >> jj) & 1) == 1].tolist())
+            exp = set() if dead[k] else set(np.nonzero(m[k])[0].tolist())
+            assert got == exp, int(qq)
+    assert (seen == 1).all()
 
 
 def test_backward_full_size_sampled_rows():
