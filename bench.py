@@ -294,6 +294,67 @@ def bench_rollout(dev, passes=10):
                     "is built on a block's first pass and reused by its later passes"}
 
 
+def bench_rollout_cfg(dev, passes=10):
+    """Config C4 with classifier-free guidance: the positive and negative
+    prompt caches (wan_video_Nplayers.py:645-648, two model calls per block
+    at :739-776) as one batch-2 paged cache, so each block is one append and
+    one attention launch over 2*H heads; against two caches of H heads and
+    two launches per block.  Same steady state as ``bench_rollout``."""
+    from multics_amd import metadata as M
+    from multics_amd.kernels import hier_attention_forward
+    from multics_amd.paged_cache import HierPagedKVCache
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS["c4"]
+    rng = np.random.default_rng(SEED)
+    _, mem, go = grouping(grp, P, T, N, rng)
+    act_full = mem.any(-1)
+    S = P * n * L + n * (N * KL + KG)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    q2, k2, v2 = ((torch.randn(S, 2 * H, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+                  for _ in range(3))
+    halves = [tuple(t[:, i * H:(i + 1) * H].contiguous() for t in (q2, k2, v2)) for i in range(2)]
+    kw = dict(num_players=P, num_groups=N, num_patches=L, num_local_hub_tokens=KL,
+              num_global_hub_tokens=KG, num_heads=H, head_dim=D, local_attn_size=W,
+              num_frame_per_block=n, device=dev)
+    both = HierPagedKVCache(batch=2, **kw)
+    pair = [HierPagedKVCache(**kw) for _ in range(2)]
+    first = (W + n) // n
+    chunk = [first, first + 1]
+    tl = {}
+    for b in range(first + 2):
+        a = act_full[b * n:b * n + n]
+        both.append(k2, v2, b * n, n, a)
+        for c, (_, kh, vh) in zip(pair, halves):
+            c.append(kh, vh, b * n, n, a)
+        if b in chunk:
+            frames, bases, lact = both.window(b * n + n - 1)
+            tl[b] = M.cached_tiles(device=dev, P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=n,
+                                   local_attn=W, frames=frames, tile_bases=bases,
+                                   local_active_frames=lact, labels=None,
+                                   q_active=act_full[b * n:b * n + n].tolist(),
+                                   direct_player=True, membership=mem, global_only=go)
+    out2 = torch.empty(S, 2 * H, D, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(S, H, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+
+    def batched():
+        for b in chunk:
+            both.append(k2, v2, b * n, n, act_full[b * n:b * n + n])
+            hier_attention_forward(q2, both.k, both.v, tl[b], out2)
+
+    def two_calls():
+        for b in chunk:
+            for c, (qh, kh, vh), o in zip(pair, halves, outs):
+                c.append(kh, vh, b * n, n, act_full[b * n:b * n + n])
+                hier_attention_forward(qh, c.k, c.v, tl[b], o)
+
+    ms_b = float(np.median(time_events(batched, passes, 3)))
+    ms_2 = float(np.median(time_events(two_calls, passes, 3)))
+    pairs = 2 * sum(tl[b].logical_pairs for b in chunk)
+    return {"players": P, "chunk_frames": 2 * n, "prompts": 2,
+            "ms_per_chunk_batched": round(ms_b, 4), "ms_per_chunk_two_calls": round(ms_2, 4),
+            "useful_tflops_batched": round(4.0 * H * D * pairs / (ms_b * 1e-3) / 1e12, 2),
+            "note": "CFG pair as one batch-2 paged cache (2*H heads per launch) vs two caches"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -411,6 +472,7 @@ def main():
                 suite[f"fwd_{cfg}"] = bench_forward_cfg(cfg, dev)
         suite["training_c5"] = bench_training(dev)
         suite["rollout_c4"] = bench_rollout(dev)
+        suite["rollout_c4_cfg"] = bench_rollout_cfg(dev)
         line["extra"]["suite"] = suite
     print(json.dumps(line), flush=True)
 

@@ -261,17 +261,22 @@ class SelfAttention(nn.Module):
                                 num_players=None, num_hub_tokens=None, cam_tokens=None,
                                 group_labels=None, active_group=None, direct_player=False,
                                 membership=None, global_only=None):
-        """One block ``x [1, P*n*L + n*(N*KL+KG), dim]`` of a cached rollout.
+        """One block ``x [B, P*n*L + n*(N*KL+KG), dim]`` of a cached rollout.
 
         Same checks and errors as the reference; the block's K/V are written
         into ``kv_cache`` (refresh in place when the block is re-run) and the
-        block attends to the cached window of every stream."""
+        block attends to the cached window of every stream.  B is 1 as in the
+        reference, or the batch of ``kv_cache`` (e.g. the positive and
+        negative prompts of classifier-free guidance, which the reference runs
+        as two calls on two caches): the members share the topology and run
+        in one attention launch."""
         if not isinstance(kv_cache, HierPagedKVCache):
             raise NotImplementedError("cached hierarchical attention runs on a "
                                       "paged_cache.HierPagedKVCache")
         b, s, dim = x.shape
-        if b != 1:
-            raise NotImplementedError("hierarchical attention supports B=1")
+        if b != kv_cache.B:
+            raise NotImplementedError("hierarchical attention supports B=1" if kv_cache.B == 1 else
+                                      f"the KV cache holds a batch of {kv_cache.B}, got B={b}")
         H, D = self.num_heads, self.head_dim
         P = int(num_players if num_players is not None else kv_cache["num_players"])
         N, KL, KG = int(kv_cache["num_groups"]), int(kv_cache["num_local_hub_tokens"]), \
@@ -321,7 +326,14 @@ class SelfAttention(nn.Module):
                 raise ValueError("hier_hub cached inference requires membership / global_only "
                                  "constant inside each latent block")
             act = act[start_frame:start_frame + n]
-        q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
+        if b == 1:
+            q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
+        else:   # batch-major heads: member i's head h is head i * H + h
+            parts = [self._qkv_blocks(x[i:i + 1], freqs,
+                                      None if cam_tokens is None else cam_tokens[i:i + 1])
+                     for i in range(b)]
+            q, k, v = (torch.stack([pt[j] for pt in parts], dim=1).view(s, b * H, D)
+                       for j in range(3))
         kv_cache.append(k, v, start_frame, n, act.numpy())
         frames, bases, lact = kv_cache.window(start_frame + n - 1)
         tiles = M.cached_tiles(
@@ -332,9 +344,10 @@ class SelfAttention(nn.Module):
             direct_player=bool(direct_player),
             membership=mem.numpy() if use_mem else None,
             global_only=go.numpy() if use_mem else None, hier_no_local_hub=no_local)
-        out = torch.zeros((s, H, D), dtype=torch.bfloat16, device=x.device)
+        out = torch.zeros((s, b * H, D), dtype=torch.bfloat16, device=x.device)
         hier_attention_forward(q, kv_cache.k, kv_cache.v, tiles, out)
-        return self.o(out.reshape(1, s, dim).to(self.o.weight.dtype))
+        out = out.view(s, b, dim).transpose(0, 1)
+        return self.o(out.to(self.o.weight.dtype))
 
     def causal_forward(self, x, freqs, mask=None, grid_sizes=None, seq_lens=None, kv_cache=None,
                        current_start=0, cache_start=None, num_frames=None, num_players=None,

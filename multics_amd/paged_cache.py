@@ -42,16 +42,26 @@ class HierPagedKVCache:
     Reads like the reference's cache dict for the keys the attention module
     inspects (``hier_hub``, ``num_players``, ``num_groups``,
     ``num_local_hub_tokens``, ``num_global_hub_tokens``, ``hier_no_local_hub``).
+
+    ``batch`` > 1 holds that many caches of the same topology in one pool,
+    interleaved per row: ``k`` / ``v`` are ``[rows, batch * H, D]``, so batch
+    member b's head h is head ``b * H + h``.  The classifier-free-guidance
+    pair of caches (wan_video_Nplayers.py:645-648, one model call per prompt
+    at :739-776) then shares the ring bookkeeping, the tile list and one
+    kernel launch per block, which sees ``batch * H`` heads.
     """
 
     def __init__(self, *, num_players: int, num_groups: int, num_patches: int,
                  num_local_hub_tokens: int, num_global_hub_tokens: int, num_heads: int,
                  head_dim: int, local_attn_size: int, num_frame_per_block: int, device,
                  dtype=torch.bfloat16, max_frames: Optional[int] = None,
-                 hier_no_local_hub: bool = False):
+                 hier_no_local_hub: bool = False, batch: int = 1):
         self.P, self.N, self.L = int(num_players), int(num_groups), int(num_patches)
         self.KL, self.KG = int(num_local_hub_tokens), int(num_global_hub_tokens)
         self.H, self.D = int(num_heads), int(head_dim)
+        self.B = int(batch)
+        if self.B < 1:
+            raise ValueError(f"batch must be >= 1, got {batch}")
         self.W, self.n = int(local_attn_size), int(num_frame_per_block)
         self.no_local = bool(hier_no_local_hub)
         if self.no_local and (self.KL != 0 or self.KG <= 0):
@@ -69,7 +79,7 @@ class HierPagedKVCache:
         self.g_rows = self.R * self.KG
         rows = self.a_rows + self.l_rows + self.g_rows
         self.device = torch.device(device)
-        self.k = torch.zeros((rows, self.H, self.D), dtype=dtype, device=self.device)
+        self.k = torch.zeros((rows, self.B * self.H, self.D), dtype=dtype, device=self.device)
         self.v = torch.zeros_like(self.k)
         self.slot_frame = np.full(self.R, -1, dtype=np.int64)
         self.local_active = np.zeros((max(self.N, 1), self.R), dtype=bool)
@@ -122,12 +132,14 @@ class HierPagedKVCache:
 
     def append(self, k_blk: torch.Tensor, v_blk: torch.Tensor, start_frame: int, n: int,
                active_block) -> None:
-        """Write a block's roped K and V ``[S_blk, H, D]`` (cached order) into
-        the pages of frames [start_frame, start_frame + n); ``active_block``
-        [n, N] are the local-hub slot flags of those frames."""
+        """Write a block's roped K and V ``[S_blk, batch * H, D]`` (cached
+        order; batch-major heads) into the pages of frames [start_frame,
+        start_frame + n); ``active_block`` [n, N] are the local-hub slot flags
+        of those frames."""
         S = self.P * n * self.L + n * ((0 if self.no_local else self.N * self.KL) + self.KG)
-        if k_blk.shape != (S, self.H, self.D) or v_blk.shape != (S, self.H, self.D):
-            raise ValueError(f"block K/V must be [{S}, {self.H}, {self.D}], "
+        HB = self.B * self.H
+        if k_blk.shape != (S, HB, self.D) or v_blk.shape != (S, HB, self.D):
+            raise ValueError(f"block K/V must be [{S}, {HB}, {self.D}], "
                              f"got {tuple(k_blk.shape)}, {tuple(v_blk.shape)}")
         if k_blk.dtype != self.k.dtype or v_blk.dtype != self.k.dtype:
             raise ValueError("block K/V dtype must match the cache")
@@ -141,7 +153,7 @@ class HierPagedKVCache:
         if k_blk.stride(2) != 1 or v_blk.stride(2) != 1:
             k_blk, v_blk = k_blk.contiguous(), v_blk.contiguous()
         args = _capi.HierPageArgs(
-            H=self.H, D=self.D, n_rows=S, pool_rows=self.k.shape[0], k_src=k_blk.data_ptr(),
+            H=HB, D=self.D, n_rows=S, pool_rows=self.k.shape[0], k_src=k_blk.data_ptr(),
             v_src=v_blk.data_ptr(), k_src_ss=k_blk.stride(0), k_src_sh=k_blk.stride(1),
             v_src_ss=v_blk.stride(0), v_src_sh=v_blk.stride(1), dst_rows=dst.data_ptr(),
             k_pool=self.k.data_ptr(), v_pool=self.v.data_ptr(), pool_ss=self.k.stride(0),

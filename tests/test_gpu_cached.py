@@ -6,7 +6,12 @@ import numpy as np
 import pytest
 import torch
 
-from multics_amd.kernels import hierarchical_paged_kv_attention, hierarchical_segmented_attention
+from multics_amd import metadata as M
+from multics_amd.kernels import (
+    hier_attention_forward,
+    hierarchical_paged_kv_attention,
+    hierarchical_segmented_attention,
+)
 from multics_amd.module import SelfAttention
 from multics_amd.paged_cache import HierPagedKVCache
 from oracle.cached import HierCacheState, cached_block_forward
@@ -147,3 +152,58 @@ def test_reference_cached_backend_call():
     with pytest.raises(RuntimeError):
         kw["roped_q"] = kw["roped_q"].clone().requires_grad_(True)
         hierarchical_paged_kv_attention(**kw)
+
+
+def test_cfg_batch_cache_matches_two_caches():
+    """A batch-2 paged cache (the classifier-free-guidance prompt pair) in one
+    launch over 2*H heads equals two caches of H heads: the pools and the
+    attention outputs bit for bit, the module's outputs up to the
+    o-projection's GEMM."""
+    need_gpu()
+    P, T, L, N, KL, KG, n, W, H, D = 4, 9, 12, 2, 2, 3, 3, 3, 2, 128
+    dim = H * D
+    m = _module(dim, H, seed=4)
+    m.num_frame_per_block, m.local_attn_size = n, W
+    kw = dict(num_players=P, num_groups=N, num_patches=L, num_local_hub_tokens=KL,
+              num_global_hub_tokens=KG, num_heads=H, head_dim=D, local_attn_size=W,
+              num_frame_per_block=n, device="cuda")
+    both = HierPagedKVCache(batch=2, **kw)
+    pair = [HierPagedKVCache(**kw) for _ in range(2)]
+    rng = np.random.default_rng(8)
+    S = P * n * L + n * (N * KL + KG)
+    g = torch.Generator().manual_seed(9)
+    for b in range(T // n):
+        lab = np.repeat(rng.integers(0, N, size=(1, P)), n, axis=0)
+        act = np.zeros((n, N), bool)
+        act[np.arange(n)[:, None], lab] = True
+        kw_b = dict(group_labels=torch.from_numpy(lab), active_group=torch.from_numpy(act),
+                    direct_player=True, current_start=b * n * P * L, num_frames=n, num_players=P)
+        ang = torch.rand(S, 1, D // 2, generator=g, dtype=torch.float64) * 6.283
+        freqs = torch.polar(torch.ones_like(ang), ang)
+        for step in range(2):
+            x = torch.randn(2, S, dim, generator=g).to("cuda", torch.bfloat16)
+            say(f"cfg batch block {b} step {step}")
+            with torch.no_grad():
+                y2 = m.causal_forward(x, freqs, kv_cache=both, **kw_b)
+                ys = [m.causal_forward(x[i:i + 1], freqs, kv_cache=c, **kw_b)
+                      for i, c in enumerate(pair)]
+            torch.cuda.synchronize()
+            for i in range(2):
+                mx, mn = err_stats(y2[i:i + 1], ys[i])
+                say(f"  member {i}: max-abs {mx:.3e} mean-abs {mn:.3e}")
+                assert mx <= 1e-2 and mn <= 1e-4
+    pools = both.k.view(both.k.shape[0], 2, H, D), both.v.view(both.v.shape[0], 2, H, D)
+    for i, c in enumerate(pair):
+        assert torch.equal(pools[0][:, i], c.k) and torch.equal(pools[1][:, i], c.v)
+    # the attention launch itself: 2*H heads in one call == H heads per call
+    frames, bases, lact = both.window(T - 1)
+    tiles = M.cached_tiles(device="cuda", P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=n,
+                           local_attn=W, frames=frames, tile_bases=bases, local_active_frames=lact,
+                           labels=lab.tolist(), q_active=act.tolist(), direct_player=True)
+    q2 = torch.randn(S, 2 * H, D, generator=g).to("cuda", torch.bfloat16)
+    out2 = torch.zeros_like(q2)
+    hier_attention_forward(q2, both.k, both.v, tiles, out2)
+    for i, c in enumerate(pair):
+        o = torch.zeros(S, H, D, dtype=torch.bfloat16, device="cuda")
+        hier_attention_forward(q2[:, i * H:(i + 1) * H].contiguous(), c.k, c.v, tiles, o)
+        assert torch.equal(out2[:, i * H:(i + 1) * H], o)
