@@ -482,6 +482,26 @@ struct SLds {
   static constexpr int SIZE = AOFF + kSteClasses * kWaves * 32 * 4;
 };
 
+// Adds a lane's 16 dS terms of one 32-key block into its class slots.  The
+// keys of a block mostly share one class (the lists keep each class's keys
+// together): a lane whose 16 keys do adds their sum once, otherwise each term.
+__device__ __forceinline__ void ste_add(float* acc, int slots, const float* ds,
+                                        const uint32_t* cls, bool valid) {
+  bool same = true;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) same = same && cls[i] == cls[0];
+  if (!valid) return;
+  if (same) {
+    float t = ds[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) t += ds[i];
+    atomicAdd(&acc[cls[0] * slots], t);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) atomicAdd(&acc[cls[i] * slots], ds[i]);
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int total) {
   __shared__ __align__(16) char lds[SLds<D>::SIZE];
@@ -558,8 +578,6 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
         s = mfma(ka[c], q[c], s);
         dp = mfma(va[c], dov[c], dp);
       }
-      // The keys of a block mostly share one class (a player's frame run):
-      // a lane whose 16 keys do adds their sum once, otherwise each term.
       float ds[16];
       uint32_t cls[16];
 #pragma unroll
@@ -575,20 +593,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
           cls[i] = cl[e] & (kSteClasses - 1);
         }
       }
-      bool same = true;
-#pragma unroll
-      for (int i = 1; i < 16; ++i) same = same && cls[i] == cls[0];
-      if (valid) {
-        if (same) {
-          float t = ds[0];
-#pragma unroll
-          for (int i = 1; i < 16; ++i) t += ds[i];
-          atomicAdd(&acc[cls[0] * kSlots], t);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) atomicAdd(&acc[cls[i] * kSlots], ds[i]);
-        }
-      }
+      ste_add(acc, kSlots, ds, cls, valid);
     }
     __syncthreads();
     if (wave == 0 && valid && lane < 32) {
@@ -642,6 +647,8 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
       for (int kb = 0; kb < 2; ++kb) {
         const f32x16 s = row_mfma<D>(q, ks, roff, kb);
         const f32x16 dp = row_mfma<D>(dov, vs, roff, kb);
+        float ds[16];
+        uint32_t cls[16];
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int k0 = kb * 32 + 8 * g4 + 4 * (lane >> 5);
@@ -651,11 +658,11 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
           for (int e = 0; e < 4; ++e) {
             const int i = 4 * g4 + e;
             const float p = __builtin_amdgcn_exp2f(fmaf(s[i], c2, -lse2));
-            const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - delta)) &
-                                             keep_mask(w[e], qframe));
-            if (valid) atomicAdd(&acc[(cl[e] & (kSteClasses - 1)) * kSlots], ds);
+            ds[i] = __uint_as_float(__float_as_uint(p * (dp[i] - delta)) & keep_mask(w[e], qframe));
+            cls[i] = cl[e] & (kSteClasses - 1);
           }
         }
+        ste_add(acc, kSlots, ds, cls, valid);
       }
     }
     wait_copies();

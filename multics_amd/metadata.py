@@ -711,9 +711,12 @@ def ste_tiles(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
             continue
         n = int(sel.sum())
         pad = -n % TILE_KEYS
-        idx_parts += [k[sel], np.zeros(pad, np.int64)]
-        mask_parts += [m[sel], np.zeros(pad, np.int64)]
-        cls_parts += [cls[sel], np.zeros(pad, np.int64)]
+        # keys grouped by class (stable), so most 32-key blocks hold one class
+        # and the pass adds one sum per lane and block
+        order = np.argsort(cls[sel], kind="stable")
+        idx_parts += [k[sel][order], np.zeros(pad, np.int64)]
+        mask_parts += [m[sel][order], np.zeros(pad, np.int64)]
+        cls_parts += [cls[sel][order], np.zeros(pad, np.int64)]
         for it in range(f0, f1):
             row = items[it].copy()
             row[5], row[6] = cursor, n + pad
