@@ -1,5 +1,5 @@
 // Paged KV cache append: scatter the K/V rows of a cached block into their
-// pool rows (one 16-byte chunk per thread, both tensors in one launch).
+// pool rows (16-byte chunks, both tensors in one launch).
 // HBM-bound copy; no row of the pool ever moves afterwards.
 #include "hier_common.h"
 
@@ -9,21 +9,25 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 
-__global__ __launch_bounds__(kThreads) void kv_append_kernel(HierPageArgs a, int64_t total) {
+// One workgroup per block row: the destination row is read once, and each
+// thread's (head, chunk) comes from 32-bit index arithmetic.
+__global__ __launch_bounds__(kThreads) void kv_append_kernel(HierPageArgs a) {
+  const int row = blockIdx.x;
+  const int dst = a.dst_rows[row];
+  if (dst < 0 || dst >= a.pool_rows) return;
   const int cpr = a.D / 8;                       // 16-byte chunks per (row, head)
-  const int64_t per_row = (int64_t)a.H * cpr;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * kThreads) {
-    const int64_t row = i / per_row;
-    const int64_t rem = i - row * per_row;
-    const int h = (int)(rem / cpr), c = (int)(rem - (int64_t)h * cpr);
-    const int dst = a.dst_rows[row];
-    if (dst < 0 || dst >= a.pool_rows) continue;
-    const int64_t po = (int64_t)dst * a.pool_ss + (int64_t)h * a.pool_sh + 8 * c;
-    *reinterpret_cast<u32x4*>(a.k_pool + po) =
-        *reinterpret_cast<const u32x4*>(a.k_src + row * a.k_src_ss + (int64_t)h * a.k_src_sh + 8 * c);
-    *reinterpret_cast<u32x4*>(a.v_pool + po) =
-        *reinterpret_cast<const u32x4*>(a.v_src + row * a.v_src_ss + (int64_t)h * a.v_src_sh + 8 * c);
+  const int per_row = a.H * cpr;
+  const uint16_t* ks = a.k_src + (int64_t)row * a.k_src_ss;
+  const uint16_t* vs = a.v_src + (int64_t)row * a.v_src_ss;
+  uint16_t* kd = a.k_pool + (int64_t)dst * a.pool_ss;
+  uint16_t* vd = a.v_pool + (int64_t)dst * a.pool_ss;
+  for (int j = threadIdx.x; j < per_row; j += kThreads) {
+    const int h = j / cpr, c = j - h * cpr;
+    const u32x4 kx = *reinterpret_cast<const u32x4*>(ks + (int64_t)h * a.k_src_sh + 8 * c);
+    const u32x4 vx = *reinterpret_cast<const u32x4*>(vs + (int64_t)h * a.v_src_sh + 8 * c);
+    const int64_t po = (int64_t)h * a.pool_sh + 8 * c;
+    *reinterpret_cast<u32x4*>(kd + po) = kx;
+    *reinterpret_cast<u32x4*>(vd + po) = vx;
   }
 }
 
@@ -45,10 +49,7 @@ extern "C" int hier_kv_append(const HierPageArgs* args, void* stream) {
   HIER_REQUIRE(a.k_src_ss % 8 == 0 && a.k_src_sh % 8 == 0 && a.v_src_ss % 8 == 0 &&
                    a.v_src_sh % 8 == 0 && a.pool_ss % 8 == 0 && a.pool_sh % 8 == 0,
                HIER_EINVAL, "strides must keep 16-byte rows aligned");
-  const int64_t total = (int64_t)a.n_rows * a.H * (a.D / 8);
-  const int64_t blocks = (total + kThreads - 1) / kThreads;
-  const int grid = (int)(blocks < 65536 ? blocks : 65536);
-  hipLaunchKernelGGL(kv_append_kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a,
-                     total);
+  HIER_REQUIRE((int64_t)a.H * (a.D / 8) < (1ll << 31), HIER_EUNSUPPORTED, "rows too wide");
+  hipLaunchKernelGGL(kv_append_kernel, dim3(a.n_rows), dim3(kThreads), 0, (hipStream_t)stream, a);
   return hier::check_launch("kv_append_kernel");
 }
