@@ -273,6 +273,32 @@ typedef struct HierPageArgs {
 
 int hier_kv_append(const HierPageArgs* args, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Frame-window attention of the action branches' cached attention: the     */
+/* F.scaled_dot_product_attention(attn_mask=...) calls of                   */
+/* blocks.py:307 (mouse temporal self-attention, one token per frame) and   */
+/* blocks.py:374 (keyboard cross-attention), whose boolean mask is          */
+/*   visible(i, j) = k_frame[j] / n_block <= q_frame[i] / n_block           */
+/*                   and (local_attn == -1 or q_frame[i] - k_frame[j] < local_attn) */
+/* (blocks.py:303-306, 366-372).  Rows that see no key are written as 0.    */
+/* Element (b, s, h, d) of q / k / v / o is at b*_sb + s*_ss + h*_sh + d.   */
+/* ------------------------------------------------------------------------ */
+typedef struct HierFrameAttnArgs {
+  int32_t B, Lq, Lk, H, D;         /* batch, queries, keys, heads, head dim (64 or 128) */
+  int32_t n_block;                 /* frames per block (>= 1)                  */
+  int32_t local_attn;              /* window in frames, -1 = unbounded         */
+  float scale;                     /* softmax scale (1/sqrt(D))                */
+  const uint16_t* q;               /* bf16                                     */
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  int64_t q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh, o_sb, o_ss, o_sh;
+  const int32_t* q_frame;          /* [Lq] DEVICE: frame of each query         */
+  const int32_t* k_frame;          /* [Lk] DEVICE: frame of each key           */
+} HierFrameAttnArgs;
+
+int hier_frame_attn(const HierFrameAttnArgs* args, void* stream);
+
 /* Last error message of the calling thread ("" if none).                    */
 const char* hier_last_error(void);
 

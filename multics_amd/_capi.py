@@ -97,6 +97,14 @@ class HierPageArgs(C.Structure):
                 ("pool_sh", i64)]
 
 
+class HierFrameAttnArgs(C.Structure):
+    _fields_ = [(n, i32) for n in ("B", "Lq", "Lk", "H", "D", "n_block", "local_attn")] + \
+               [("scale", f32)] + [(n, vp) for n in ("q", "k", "v", "o")] + \
+               [(n, i64) for n in ("q_sb", "q_ss", "q_sh", "k_sb", "k_ss", "k_sh", "v_sb", "v_ss",
+                                   "v_sh", "o_sb", "o_ss", "o_sh")] + \
+               [("q_frame", vp), ("k_frame", vp)]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
@@ -104,6 +112,7 @@ EXPORTS = {
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],
     "hier_kv_append": [C.POINTER(HierPageArgs), vp],
+    "hier_frame_attn": [C.POINTER(HierFrameAttnArgs), vp],
     "hier_last_error": [],
     "hier_version": [],
 }
