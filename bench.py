@@ -355,6 +355,44 @@ def bench_rollout_cfg(dev, passes=10):
             "note": "CFG pair as one batch-2 paged cache (2*H heads per launch) vs two caches"}
 
 
+def bench_action_temporal(dev, passes=20):
+    """The mouse branch's cached temporal attention at C4 scale
+    (blocks.py:256-308): one sequence per spatial token of every player
+    (P*L = 2,200), the block's 3 frames attending to the cached window of
+    W + n = 24 frames, 24 heads of 128.  HIP frame-window attention against
+    the reference's ``F.scaled_dot_product_attention(attn_mask=...)`` on the
+    same GPU; HBM-bound on reading the window once."""
+    from multics_amd.action import frame_attention
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS["c4"]
+    B, f, win = P * L, n, W + n
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    q = (torch.randn(B, f, H, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(B, win, H, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    v = torch.randn(B, win, H, D, generator=g, device=dev).to(torch.bfloat16)
+    start = 2 * W                                     # a steady-state block: window full
+    qf = torch.arange(start, start + f)
+    kf = torch.arange(start + f - win, start + f)
+    qf_d, kf_d = qf.to(torch.int32).to(dev), kf.to(torch.int32).to(dev)
+    mask = ((kf[None, :] // n) <= (qf[:, None] // n)) & ((qf[:, None] - kf[None, :]) < W)
+    mask = mask.to(dev)
+    qt, kt, vt = (t.transpose(1, 2) for t in (q, k, v))
+    ms_hip = float(np.median(time_events(lambda: frame_attention(q, k, v, qf_d, kf_d, n, W),
+                                         passes, 3)))
+    ms_sdpa = float(np.median(time_events(
+        lambda: torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask),
+        passes, 3)))
+    got = frame_attention(q, k, v, qf_d, kf_d, n, W).float()
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask)
+    diff = (got - ref.transpose(1, 2).float()).abs().max().item()
+    bytes_ = 2 * (2 * B * win * H * D + 2 * B * f * H * D)
+    return {"sequences": B, "queries_per_seq": f, "window_frames": win, "heads": H, "head_dim": D,
+            "ms_hip": round(ms_hip, 4), "ms_torch_sdpa": round(ms_sdpa, 4),
+            "hbm_gb_per_call": round(bytes_ / 1e9, 3),
+            "achieved_gbs": round(bytes_ / (ms_hip * 1e-3) / 1e9, 1),
+            "frac_hbm": round(bytes_ / (ms_hip * 1e-3) / 8e12, 4),
+            "max_abs_vs_sdpa": round(diff, 5)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -473,6 +511,7 @@ def main():
         suite["training_c5"] = bench_training(dev)
         suite["rollout_c4"] = bench_rollout(dev)
         suite["rollout_c4_cfg"] = bench_rollout_cfg(dev)
+        suite["action_temporal_c4"] = bench_action_temporal(dev)
         line["extra"]["suite"] = suite
     print(json.dumps(line), flush=True)
 
