@@ -3,10 +3,9 @@
 // keyboard cross-attention over a rolling cache).  The sequences are short
 // (a few queries per sequence and head against at most a few hundred cached
 // keys), so instead of the tile kernel's 32 x 32 MFMA blocks a wave serves
-// one (batch, head) and 64 / (D/8) queries: each query owns D/8 lanes, each
-// lane 8 channels.  A key's row is read once per wave (the query groups read
-// the same 16-byte chunks), the partial dot products are summed across the
-// query's lanes, and the softmax runs online in fp32.  For the temporal
+// 64 / (D/8) (sequence, query) slots of one head: each query owns D/8 lanes,
+// each lane 8 channels.  The partial dot products are summed across the
+// query's lanes and the softmax runs online in fp32.  For the temporal
 // branch the kernel is bound by reading the cached window once.
 #include "hier_common.h"
 
@@ -26,12 +25,17 @@ template <int D>
 __global__ __launch_bounds__(64) void frame_attn_kernel(HierFrameAttnArgs a) {
   constexpr int LPQ = D / 8;          // lanes per query
   constexpr int QPW = 64 / LPQ;       // queries per wave
+  // the wave's query slots run over (batch, query) pairs, so sequences with
+  // fewer queries than slots share a wave; each slot reads its own
+  // sequence's keys (slots of one sequence read the same rows)
   const int lane = threadIdx.x;
   const int c = lane % LPQ;
-  const int qi = blockIdx.x * QPW + lane / LPQ;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const bool valid = qi < a.Lq;
-  const int qs = valid ? qi : 0;
+  const int slot = blockIdx.x * QPW + lane / LPQ;
+  const int h = blockIdx.y;
+  const bool valid = slot < a.B * a.Lq;
+  const int b = valid ? slot / a.Lq : 0;
+  const int qi = valid ? slot - b * a.Lq : 0;
+  const int qs = qi;
   const u32x4 qw = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + qs * a.q_ss + h * a.q_sh + 8 * c);
   const int qf = a.q_frame[qs];
   const int qblk = qf / a.n_block;
@@ -114,9 +118,11 @@ extern "C" int hier_frame_attn(const HierFrameAttnArgs* args, void* stream) {
                    a.k_ss % 8 == 0 && a.k_sh % 8 == 0 && a.v_sb % 8 == 0 && a.v_ss % 8 == 0 &&
                    a.v_sh % 8 == 0 && a.o_sb % 8 == 0 && a.o_ss % 8 == 0 && a.o_sh % 8 == 0,
                HIER_EINVAL, "strides must keep 16-byte rows aligned");
-  HIER_REQUIRE(a.H <= 65535 && a.B <= 65535, HIER_EUNSUPPORTED, "at most 65535 heads / batch");
+  HIER_REQUIRE(a.H <= 65535, HIER_EUNSUPPORTED, "at most 65535 heads");
   const int qpw = 64 / (a.D / 8);
-  const dim3 grid((a.Lq + qpw - 1) / qpw, a.H, a.B);
+  const int64_t slots = (int64_t)a.B * a.Lq;
+  HIER_REQUIRE(slots / qpw < (1ll << 31) - 1, HIER_EUNSUPPORTED, "too many queries");
+  const dim3 grid((unsigned)((slots + qpw - 1) / qpw), a.H, 1);
   if (a.D == 128)
     hipLaunchKernelGGL(frame_attn_kernel<128>, grid, dim3(64), 0, (hipStream_t)stream, a);
   else
