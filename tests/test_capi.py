@@ -81,6 +81,25 @@ def test_null_arguments_are_rejected_without_a_gpu():
     assert lib.hier_qkv_prologue(None, None) == _capi.HIER_EINVAL
     assert lib.hier_meta_count(None, None, None) == _capi.HIER_EINVAL
     assert lib.hier_meta_build(None, None, None) == _capi.HIER_EINVAL
+    assert lib.hier_kv_append(None, None) == _capi.HIER_EINVAL
+    assert lib.hier_frame_attn(None, None) == _capi.HIER_EINVAL
+
+
+def test_frame_attention_argument_checks_without_a_gpu():
+    """Invalid shapes are refused and an empty batch returns before any
+    launch (nothing here is dereferenced)."""
+    lib = _capi.lib()
+    fake = 1 << 20
+    a = _capi.HierFrameAttnArgs(B=0, Lq=3, Lk=24, H=2, D=128, n_block=3, local_attn=21,
+                                scale=0.088, q=fake, k=fake, v=fake, o=fake, q_frame=fake,
+                                k_frame=fake)
+    assert lib.hier_frame_attn(C.byref(a), None) == _capi.HIER_OK
+    a.D = 96
+    assert lib.hier_frame_attn(C.byref(a), None) == _capi.HIER_EUNSUPPORTED
+    a.D, a.local_attn = 128, 0
+    assert lib.hier_frame_attn(C.byref(a), None) == _capi.HIER_EINVAL
+    a.local_attn, a.n_block = 21, 0
+    assert lib.hier_frame_attn(C.byref(a), None) == _capi.HIER_EINVAL
 
 
 def test_forward_rejects_views_past_the_24_bit_row_limit_without_a_gpu():
