@@ -119,6 +119,46 @@ def build_case(cfg, device):
     return topo, res.tiles, host_build_s, (first, mem, go)
 
 
+def camera_tokens(P, T, L, K, dev, pos_scale=1.0):
+    """Camera12 tokens ``[S, 12]`` bf16 of seeded per-frame poses: yaw ~
+    U(-180, 180) deg, pitch ~ U(-30, 30) deg, position a random walk with
+    N(0, 0.05) m steps; anchored at player 0 frame 0 (dataset.py:49-90,
+    raw_inputs.py:250-273), broadcast to each frame's L tokens, zero rows for
+    the K hub tokens per frame (blocks.py:108-148)."""
+    from multics_amd.camera import build_camera_tokens, camera12_from_absolute_c2w, camera_to_world
+    rng = np.random.default_rng(SEED + 1)
+    pose = np.zeros((P, T, 5))
+    pose[..., :3] = np.cumsum(rng.normal(0.0, 0.05, (P, T, 3)), axis=1)
+    pose[..., 3] = rng.uniform(-180.0, 180.0, (P, T))
+    pose[..., 4] = rng.uniform(-30.0, 30.0, (P, T))
+    c12 = camera12_from_absolute_c2w(torch.from_numpy(camera_to_world(pose)), pos_scale)
+    ref = torch.empty(1, 0, dtype=torch.bfloat16, device=dev)
+    return build_camera_tokens(c12, T, L, P, ref, include_hub=True, num_hub_tokens=K)[0].contiguous()
+
+
+def rope_tables(P, T, L, K, D, dev):
+    """fp32 cos / sin ``[S, D/2]`` of the simplex 4D RoPE table of a full
+    sequence (pool of 10 vertices, vertex id = player index, 11 x 20 patch
+    grid; WanModel.build_self_attn_freqs_with_hub, wan_video_dit.py:338-359)."""
+    from multics_amd import rope
+    h, w = (11, 20) if L == 220 else (1, L)
+    bands = rope.precompute_freqs_cis_4d_wan_rerope(D)
+    verts = rope.build_simplex_vertices(10, rope.WAN_REROPE_SPLITS[1])
+    freqs = rope.build_self_attn_freqs_with_hub(bands, verts, T, h, w, "cpu", list(range(P)), K)
+    return rope.freqs_to_cos_sin(freqs, device=dev)
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), else the machine type."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def profiled_traffic(cfg):
     """HBM bytes per launch of the forward kernel from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of the same workload (counter values scaled
@@ -181,7 +221,7 @@ def cpu_baseline(cfg, topo_args, budget_s=20.0):
     return dict(ms_layer=ms_layer, sample=f"{done} head(s) of temporal block {b} of {T // n} "
                 f"({len(rows)} query rows x {S} keys, dense mask SDPA fp32), extrapolated x"
                 f"{(T // n) * H / done:.0f}", cores=cores, threads=torch.get_num_threads(),
-                cpu=platform.processor() or platform.machine())
+                cpu=cpu_model())
 
 
 def bench_forward_cfg(cfg, dev, steps=10, warmup=3):
@@ -445,18 +485,17 @@ def main():
     useful_flop = 4.0 * H * D * tiles.logical_pairs
     tflops = useful_flop / (ms * 1e-3) / 1e12
 
-    # fused Q/K prologue (camera + RMSNorm + RoPE) on the same sequence
+    # fused Q/K prologue (camera + RMSNorm + RoPE) on the same sequence: camera12
+    # tokens of seeded poses and the simplex 4D RoPE table of the layout
     dim = H * D
     qx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
     kx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
     vx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
-    cam = torch.zeros(S, 12, device=dev, dtype=torch.bfloat16)
-    cam[:P * T * L] = torch.randn(P * T * L, 12, generator=g, device=dev).to(torch.bfloat16)
+    cam = camera_tokens(P, T, L, N * KL + KG, dev)
     wcq = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
     wck = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
     nw = torch.ones(dim, dtype=torch.bfloat16, device=dev)
-    ang = torch.rand(S, D // 2, generator=g, device=dev) * 6.28
-    cs, sn = torch.cos(ang), torch.sin(ang)
+    cs, sn = rope_tables(P, T, L, N * KL + KG, D, dev)
     pro = time_events(lambda: qkv_prologue(qx, kx, vx, norm_q_w=nw, norm_k_w=nw, rope_cos=cs,
                                            rope_sin=sn, num_heads=H, eps=1e-6, cam=cam,
                                            w_cam_q=wcq, w_cam_k=wck, out_layout="hsd"),

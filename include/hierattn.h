@@ -138,7 +138,7 @@ int hier_meta_build(const HierTopo* topo, const HierMetaOut* out, void* stream);
 /* (multics/models/rope.py:248-254).                                         */
 /* ------------------------------------------------------------------------ */
 typedef struct HierPrologueArgs {
-  int32_t S, H, D;                 /* tokens, heads, head dim (D = 128)       */
+  int32_t S, H, D;                 /* tokens, heads, head dim (64 or 128)     */
   float eps;                       /* RMSNorm epsilon                          */
   const uint16_t* qx;              /* [S][H*D] bf16 q(x) (with bias)           */
   const uint16_t* kx;              /* [S][H*D] bf16 k(x)                       */
@@ -167,7 +167,7 @@ int hier_qkv_prologue(const HierPrologueArgs* args, void* stream);
 /* hier_packed_attention.py:230-242).  Rows with no visible key are 0.       */
 /* ------------------------------------------------------------------------ */
 typedef struct HierFwdArgs {
-  int32_t H, D;                    /* heads, head dim (must be 128)            */
+  int32_t H, D;                    /* heads, head dim (64 or 128)              */
   int32_t n_items;                 /* work items (tile_items rows)             */
   float scale;                     /* softmax scale (1/sqrt(D))                */
   int32_t kv_rows;                 /* rows addressable in k / v (> every key index) */

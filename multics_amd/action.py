@@ -92,6 +92,10 @@ def frame_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_frame: 
     n_block`` and, for ``local_attn != -1``, ``q_frame[i] - k_frame[j] <
     local_attn``.  Returns ``[B, Lq, H, D]`` bf16 (0 for a query that sees
     no key)."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise RuntimeError("frame-window attention is inference-only (q/k/v require grad); run "
+                           "the cached action branches under torch.no_grad() or "
+                           "torch.inference_mode()")
     for name, t in (("q", q), ("k", k), ("v", v)):
         if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() != 4 or t.stride(3) != 1:
             raise NotImplementedError(f"{name} must be a bf16 GPU tensor [B, L, H, D] with unit "

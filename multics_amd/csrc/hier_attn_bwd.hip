@@ -29,6 +29,7 @@
 // the accumulators to bf16 operands without any shuffle.  Tiles are copied
 // with global_load_lds_dwordx4 into the swizzled layouts of hier_tile.h.
 #include "hier_common.h"
+#include "hier_launch.h"
 #include "hier_tile.h"
 
 namespace {
@@ -187,9 +188,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   __shared__ __align__(16) char lds_v0[Geo<D>::TILEB], lds_v1[Geo<D>::TILEB];
   __shared__ __align__(16) char lds_m0[Geo<D>::MBYTES], lds_m1[Geo<D>::MBYTES];
   const QStages st = {{lds_k0, lds_k1}, {lds_v0, lds_v1}, {lds_m0, lds_m1}};
-  const int G = gridDim.x;
-  const int bid = blockIdx.x;
-  const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
   if (logical >= total) return;
   const int head = logical / a.n_items;
   const int item = logical - head * a.n_items;
@@ -393,9 +392,7 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(HierBwdArgs a, int to
   __shared__ __align__(16) char lds_d0[Geo<D>::TILEB], lds_d1[Geo<D>::TILEB];
   __shared__ __align__(16) char lds_w0[3 * Geo<D>::MBYTES], lds_w1[3 * Geo<D>::MBYTES];
   const KStages st = {{lds_q0, lds_q1}, {lds_d0, lds_d1}, {lds_w0, lds_w1}};
-  const int G = gridDim.x;
-  const int bid = blockIdx.x;
-  const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
   if (logical >= total) return;
   const int head = logical / a.n_key_items;
   const int item = logical - head * a.n_key_items;
@@ -505,9 +502,7 @@ __device__ __forceinline__ void ste_add(float* acc, int slots, const float* ds,
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int total) {
   __shared__ __align__(16) char lds[SLds<D>::SIZE];
-  const int G = gridDim.x;
-  const int bid = blockIdx.x;
-  const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
   if (logical >= total) return;
   const int head = logical / a.n_ste_items;
   const int item = logical - head * a.n_ste_items;
@@ -718,14 +713,14 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
     HIER_REQUIRE(a.ste_classes >= 1 && a.ste_classes <= kSteClasses, HIER_EUNSUPPORTED,
                  "membership STE supports 1..%d classes (groups / players), got %d", kSteClasses,
                  a.ste_classes);
-    HIER_REQUIRE((int64_t)a.n_ste_items * a.H < (1ll << 31) - 8, HIER_EUNSUPPORTED,
+    HIER_REQUIRE((int64_t)a.n_ste_items * a.H <= hier::kMaxLaunchItems, HIER_EUNSUPPORTED,
                  "too many work items");
   }
   const int64_t tq = (int64_t)a.n_items * a.H, tk = (int64_t)a.n_key_items * a.H;
-  HIER_REQUIRE(tq < (1ll << 31) - 8 && tk < (1ll << 31) - 8, HIER_EUNSUPPORTED, "too many work items");
+  HIER_REQUIRE(tq <= hier::kMaxLaunchItems && tk <= hier::kMaxLaunchItems, HIER_EUNSUPPORTED, "too many work items");
   hipStream_t s = (hipStream_t)stream;
   if (tq > 0) {
-    const int grid = (int)((tq + 7) / 8 * 8);
+    const int grid = (int)hier::xcd_grid(tq);
     if (a.D == 128)
       hipLaunchKernelGGL(dq_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
     else
@@ -734,7 +729,7 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
     if (rc != HIER_OK) return rc;
   }
   if (tk > 0) {
-    const int grid = (int)((tk + 7) / 8 * 8);
+    const int grid = (int)hier::xcd_grid(tk);
     if (a.D == 128) {
       hipLaunchKernelGGL((dkdv_kernel<128, kPassDV>), dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
       hipLaunchKernelGGL((dkdv_kernel<128, kPassDK>), dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
@@ -747,7 +742,7 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
   }
   const int64_t ts = (int64_t)a.n_ste_items * a.H;
   if (a.n_ste_items > 0) {
-    const int grid = (int)((ts + 7) / 8 * 8);
+    const int grid = (int)hier::xcd_grid(ts);
     if (a.D == 128)
       hipLaunchKernelGGL(ste_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)ts);
     else

@@ -36,6 +36,7 @@
 //
 // The LDS tile layout and the copies are described in hier_tile.h.
 #include "hier_common.h"
+#include "hier_launch.h"
 #include "hier_tile.h"
 
 namespace {
@@ -324,9 +325,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
   // XCD-aware mapping: consecutive logical items land on the same XCD (the
   // dispatcher round-robins workgroups over 8 XCDs), so items sharing a head
   // and overlapping key windows share one L2.
-  const int G = gridDim.x;
-  const int bid = blockIdx.x;
-  const int logical = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
   if (logical >= total) return;
   const int head = logical / a.n_items;
   const int item = logical - head * a.n_items;
@@ -446,8 +445,8 @@ extern "C" int hier_attn_fwd(const HierFwdArgs* args, void* stream) {
                HIER_EUNSUPPORTED, "K/V need at most 2^24 rows and a row stride under 8M elements");
   if (a.n_items == 0) return HIER_OK;
   const int64_t total = (int64_t)a.n_items * a.H;
-  HIER_REQUIRE(total < (1ll << 31) - 8, HIER_EUNSUPPORTED, "too many work items");
-  const int grid = (int)((total + 7) / 8 * 8);
+  HIER_REQUIRE(total <= hier::kMaxLaunchItems, HIER_EUNSUPPORTED, "too many work items");
+  const int grid = (int)hier::xcd_grid(total);
   if (a.D == 128)
     hipLaunchKernelGGL(attn_fwd_kernel<128>, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a,
                        (int)total);

@@ -155,7 +155,9 @@ class SelfAttention(nn.Module):
                 and self.head_dim in (64, 128))
 
     def _project_fused(self, x, freqs, cam_tokens=None):
-        """No-grad Q/K/V: GEMMs, then the fused HIP prologue.  Returns [S, H, D]."""
+        """No-grad Q/K/V: GEMMs, then the fused HIP prologue.  Returns [S, H, D]
+        views of head-major storage (each head's rows one contiguous slab, the
+        layout the attention kernel gathers keys from fastest)."""
         cam = self._check_cam(x, cam_tokens)
         qx, kx, vx = (lin(x)[0].contiguous() for lin in (self.q, self.k, self.v))
         cs, sn = freqs_to_cos_sin(freqs, device=x.device)
@@ -164,7 +166,7 @@ class SelfAttention(nn.Module):
             rope_sin=sn, num_heads=self.num_heads, eps=self.norm_q.eps,
             cam=None if cam is None else cam[0],
             w_cam_q=None if cam is None else self.cam_q.weight,
-            w_cam_k=None if cam is None else self.cam_k.weight)
+            w_cam_k=None if cam is None else self.cam_k.weight, out_layout="hsd")
 
     def _qkv_blocks(self, x, freqs, cam_tokens):
         """[S, H, D] bf16 Q/K/V of a [1, S, dim] input (fused prologue when it applies)."""
@@ -273,6 +275,14 @@ class SelfAttention(nn.Module):
         if not isinstance(kv_cache, HierPagedKVCache):
             raise NotImplementedError("cached hierarchical attention runs on a "
                                       "paged_cache.HierPagedKVCache")
+        if torch.is_grad_enabled() and (x.requires_grad or
+                                        any(p.requires_grad for p in self.parameters())):
+            # the reference's cached backends refuse autograd the same way
+            # (hier_paged_attention.py:123-124); its cached rollouts run under
+            # torch.inference_mode (training.py:1112)
+            raise RuntimeError("cached hierarchical attention is inference-only (autograd is "
+                               "enabled and the input or the weights require grad); run it "
+                               "under torch.no_grad() or torch.inference_mode()")
         b, s, dim = x.shape
         if b != kv_cache.B:
             raise NotImplementedError("hierarchical attention supports B=1" if kv_cache.B == 1 else

@@ -145,6 +145,11 @@ class HierPagedKVCache:
             raise ValueError("block K/V dtype must match the cache")
         if n > self.R:
             raise ValueError(f"a block of {n} frames does not fit a window of {self.R} frames")
+        if self.W == -1 and (start_frame < 0 or start_frame + n > self.R):
+            # an unbounded window keeps every frame: a ring slot may never be
+            # reused, or the window would silently lose its oldest frames
+            raise ValueError(f"frames [{start_frame}, {start_frame + n}) exceed the cache's "
+                             f"max_frames={self.R} (local_attn_size=-1 keeps every frame)")
         key = (start_frame % self.R, n)
         dst = self._dst_cache.get(key)
         if dst is None:

@@ -64,3 +64,50 @@ def ste_attention(q, k, v, topo: FullTopology, logits: torch.Tensor, scale=None)
     p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
     o = torch.einsum("hqk,khd->qhd", p, v.float())
     return o * live[:, None, None]
+
+
+def ste_grad_at(q, k, v, dout, topo: FullTopology, logits: torch.Tensor, bits, scale=None):
+    """dL/dlogit of ``sum(ste_attention(q, k, v, topo, logits) * dout)`` at the
+    membership bits ``bits`` (an iterable of (t, g, p)), without the S x S
+    pass: only the rows whose edges a bit gates are evaluated.
+
+    The bias of bit (t, g, p) sits on two edge sets (see ``gate_index``):
+    player p's rows at frame t to every local-hub key of group g, and group
+    g's hub rows at frame t to every key of player p.  With the bias zero in
+    value, dL/dbias_ij = dS_ij = P_ij (dP_ij - delta_i) (dP_ij = dO_i.v_j,
+    delta_i = dO_i.O_i), summed over heads because the bias is shared by all
+    heads, so dL/dlogit = sigmoid'(logit) * sum of dS over those edges.
+    Inactive local-hub rows output 0 (their dO counts as 0).  Returns a float64
+    numpy array, one value per bit.
+    """
+    S, H, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    P, T, L, N, KL = topo.P, topo.T, topo.L, topo.N, topo.KL
+    qf, kf, vf, df = (t.float() for t in (q, k, v, dout))
+    dead = inactive_local_rows(topo)
+    kind, _, kp, kg = topo.token_ids(np.arange(S))
+    a0 = P * T * L
+    lg = logits.detach().double().reshape(T, N, P)
+    out = []
+    for (t, g, p) in bits:
+        total = 0.0
+        player_rows = p * T * L + t * L + np.arange(L)
+        local_rows = a0 + (t * N + g) * KL + np.arange(KL)
+        for rows, gated in ((player_rows, (kind == 1) & (kg == g)),
+                            (local_rows, (kind == 0) & (kp == p))):
+            rows = rows[~dead[rows]]
+            if len(rows) == 0:
+                continue
+            rt = torch.from_numpy(rows)
+            m = torch.from_numpy(mask_rows(topo, q_idx=rows))                 # [r, S]
+            s = torch.einsum("qhd,khd->hqk", qf[rt], kf) * scale
+            s = s.masked_fill(~m[None], float("-inf"))
+            pr = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)          # [H, r, S]
+            o = torch.einsum("hqk,khd->qhd", pr, vf)
+            delta = (df[rt] * o).sum(-1)                                      # [r, H]
+            dp = torch.einsum("qhd,khd->hqk", df[rt], vf)
+            ds = pr * (dp - delta.T[:, :, None])
+            total += float(ds[:, :, torch.from_numpy(gated)].double().sum())
+        sig = 1.0 / (1.0 + math.exp(-float(lg[t, g, p])))
+        out.append(sig * (1.0 - sig) * total)
+    return np.array(out, dtype=np.float64)

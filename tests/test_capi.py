@@ -21,6 +21,7 @@ STRUCTS = {
     "HierFwdArgs": _capi.HierFwdArgs,
     "HierBwdArgs": _capi.HierBwdArgs,
     "HierPageArgs": _capi.HierPageArgs,
+    "HierFrameAttnArgs": _capi.HierFrameAttnArgs,
 }
 
 

@@ -11,7 +11,8 @@ from ``oracle.attention.attention_grads_at``; the C4 rollout (paged KV cache,
 window full) compares sampled rows of its last blocks with the full-sequence
 oracle, which an in-order rollout equals.  Tolerances as in the small
 cases: forward max-abs 2e-2 / mean-abs 2e-3, log-sum-exp within 2^-8;
-gradients within 2 % of the reference's max and 1 % of its mean.
+gradients max-abs 2e-2 / mean-abs 2e-3 and within 2 % of the reference's
+max and 1 % of its mean.
 """
 
 import math
@@ -99,6 +100,43 @@ def test_forward_full_size_sampled_rows(cfg):
     _check_key_sets(tiles, rows, m.numpy(), ~live.numpy())
 
 
+def test_forward_c2_as_benchmarked():
+    """The headline configuration exactly as ``bench.py`` times it: C2 with
+    all 24 heads, Q/K/V stored head-major (``[H, S, D]`` presented as
+    ``[S, H, D]`` views, the layout ``qkv_prologue(out_layout="hsd")`` and
+    the module's no-grad path write).  Sampled rows against the oracle at the
+    north-star bounds; the whole output bit-identical to the same forward on
+    token-major ``[S, H, D]`` copies of the inputs (the layout changes only the
+    addresses the kernel reads)."""
+    need_gpu()
+    meta, topo, D = _case("c2")
+    H = bench.CONFIGS["c2"][8]
+    assert H == 24
+    say("c2 as benchmarked: S", topo.S, "H", H)
+    tiles = M.build(meta, "cuda").tiles
+    g = torch.Generator().manual_seed(31)
+    qh, kh, vh = ((torch.randn(H, topo.S, D, generator=g) * 0.5).to(torch.bfloat16)
+                  for _ in range(3))
+    qd, kd, vd = (t.cuda().permute(1, 0, 2) for t in (qh, kh, vh))
+    assert qd.stride() == (D, topo.S * D, 1)
+    out = torch.zeros(topo.S, H, D, dtype=torch.bfloat16, device="cuda")
+    hier_attention_forward(qd, kd, vd, tiles, out)
+    torch.cuda.synchronize()
+    say("  head-major done; token-major copies")
+    out_shd = torch.zeros_like(out)
+    hier_attention_forward(qd.contiguous(), kd.contiguous(), vd.contiguous(), tiles, out_shd)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_shd)
+    rows = _rows(topo, np.random.default_rng(8), n_random=96)
+    rt = torch.from_numpy(rows)
+    say(f"  {len(rows)} sampled rows x {H} heads against the oracle")
+    q, k, v = (t.permute(1, 0, 2) for t in (qh, kh, vh))
+    ref = masked_attention(q, k, v, topo, rows=rows)
+    mx, mn = err_stats(out.cpu()[rt], ref)
+    say(f"  max-abs {mx:.3e} mean-abs {mn:.3e}")
+    assert mx <= MAX_ABS and mn <= MEAN_ABS
+
+
 def _check_key_sets(tiles, rows, m, dead):
     items = tiles.items[:tiles.n_items].cpu().numpy()
     idx = tiles.kv_idx.cpu().numpy()
@@ -131,6 +169,50 @@ def test_backward_full_size_sampled_rows():
     rows = _rows(topo, np.random.default_rng(6))
     rt = torch.from_numpy(rows)
     say(f"  {len(rows)} sampled rows")
+    dq, dk, dv = attention_grads_at(q, k, v, dout, topo, q_rows=rows, k_rows=rows)
+    _check("dq", qd.grad.cpu()[rt], dq)
+    _check("dk", kd.grad.cpu()[rt], dk)
+    _check("dv", vd.grad.cpu()[rt], dv)
+
+
+def test_membership_gradient_full_size_sampled_bits():
+    """C5 with soft membership logits ~ N(0, 1): the logit gradient of the HIP
+    STE pass at sampled membership bits (on and off) against the row-sampled
+    fp32 oracle ``oracle.ste.ste_grad_at`` (pinned to the autograd
+    definition), plus dQ / dK / dV at sampled rows; north-star bounds."""
+    need_gpu()
+    from oracle.ste import ste_grad_at
+    P, T, L, N, KL, KG, n, W, _, D, grp = bench.CONFIGS["c5"]
+    logits, mem, go = bench.grouping(grp, P, T, N, np.random.default_rng(bench.SEED))
+    topo = FullTopology(P, T, L, N, KL, KG, n, W, True, membership=mem, global_only=go)
+    meta = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W, direct=True,
+                                    membership=mem, global_only=go)
+    H = 4
+    say("full-size membership gradient c5 S", topo.S, "H", H)
+    tiles = M.build(meta, "cuda").tiles
+    q, k, v = _inputs(topo.S, H, D, seed=41)
+    dout = torch.randn(topo.S, H, D, generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    lg = torch.from_numpy(logits).float().cuda().requires_grad_(True)
+    out = hier_attention(qd, kd, vd, tiles, membership_logits=lg, ste_geometry=(P, T, L, N, KL))
+    out.backward(dout.cuda())
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(9)
+    on = np.argwhere(mem)
+    off = np.argwhere(~mem)
+    bits = [tuple(int(x) for x in b) for b in on[rng.choice(len(on), 10, replace=False)]]
+    bits += [tuple(int(x) for x in b) for b in off[rng.choice(len(off), 3, replace=False)]]
+    say(f"  {len(bits)} sampled bits")
+    want = ste_grad_at(q, k, v, dout, topo, torch.from_numpy(logits).float(), bits)
+    got = lg.grad.cpu().double().numpy()[tuple(np.array(bits).T)]
+    err = np.abs(got - want)
+    say(f"  dlogits max-abs {err.max():.3e} mean-abs {err.mean():.3e} (ref max "
+        f"{np.abs(want).max():.3e})")
+    assert np.isfinite(got).all() and np.abs(want[:10]).max() > 0
+    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS
+    assert (got[10:] == 0).all()      # bits that are off gate no edge
+    rows = _rows(topo, np.random.default_rng(10), n_random=32)
+    rt = torch.from_numpy(rows)
     dq, dk, dv = attention_grads_at(q, k, v, dout, topo, q_rows=rows, k_rows=rows)
     _check("dq", qd.grad.cpu()[rt], dq)
     _check("dk", kd.grad.cpu()[rt], dk)

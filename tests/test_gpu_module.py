@@ -45,6 +45,10 @@ def _rel(a, b):
     return ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-12)).item()
 
 
+def _rel_mean(a, b):
+    return ((a.float() - b.float()).abs().mean() / b.float().abs().mean().clamp_min(1e-12)).item()
+
+
 def test_forward_hier_tiled_ste_training_and_inference():
     need_gpu()
     P, T, L, N, KL, KG, n, W, H, D = 4, 6, 20, 2, 5, 6, 3, 4, 2, 128
@@ -92,8 +96,9 @@ def test_forward_hier_tiled_ste_training_and_inference():
 
 def test_module_gradients_match_fp32_autograd():
     """dL/dx and dL/dW_v through the HIP backward against fp32 autograd of the
-    same module math with the oracle attention (relative bound 5e-2 on the
-    largest entry: bf16 projections on one side, fp32 on the other)."""
+    same module math with the oracle attention: max error <= 2e-2 x the
+    largest entry, mean error <= 1e-2 x the mean magnitude (bf16 projections
+    and bf16 weight gradients on one side, fp32 on the other)."""
     need_gpu()
     P, T, L, N, KL, KG, n, W, H, D = 2, 3, 16, 2, 2, 2, 3, -1, 2, 64
     dim = H * D
@@ -126,9 +131,9 @@ def test_module_gradients_match_fp32_autograd():
     say(f"  dx rel {_rel(xg.grad.cpu(), xf.grad):.3e}  dWv rel "
         f"{_rel(m.v.weight.grad.cpu(), mf.v.weight.grad):.3e}  dWq rel "
         f"{_rel(m.q.weight.grad.cpu(), mf.q.weight.grad):.3e}")
-    assert _rel(xg.grad.cpu(), xf.grad) < 5e-2
-    assert _rel(m.v.weight.grad.cpu(), mf.v.weight.grad) < 5e-2
-    assert _rel(m.q.weight.grad.cpu(), mf.q.weight.grad) < 5e-2
+    for got, want in ((xg.grad.cpu(), xf.grad), (m.v.weight.grad.cpu(), mf.v.weight.grad),
+                      (m.q.weight.grad.cpu(), mf.q.weight.grad)):
+        assert _rel(got, want) < 2e-2 and _rel_mean(got, want) < 1e-2
 
 
 def test_forward_hier_membership_logits():
@@ -164,4 +169,6 @@ def test_forward_hier_membership_logits():
     mx, _ = err_stats(y.detach(), yo.detach())
     say(f"  output max-abs {mx:.3e}  dlogits rel {_rel(lg.grad.cpu(), lf.grad):.3e}")
     assert mx <= 2e-2
-    assert _rel(lg.grad.cpu(), lf.grad) < 5e-2
+    err = (lg.grad.cpu() - lf.grad).abs()
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3
+    assert _rel(lg.grad.cpu(), lf.grad) < 2e-2

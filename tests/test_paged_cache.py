@@ -53,3 +53,41 @@ def test_no_local_layout_and_errors():
         HierPagedKVCache(num_players=2, num_groups=2, num_patches=4, num_local_hub_tokens=2,
                          num_global_hub_tokens=2, num_heads=1, head_dim=8, local_attn_size=-1,
                          num_frame_per_block=3, device="cpu")
+
+
+def test_unbounded_window_refuses_to_wrap():
+    """local_attn_size=-1 keeps every frame: appending past max_frames must
+    fail instead of overwriting the oldest pages (the reference's buffer
+    has no wrap either)."""
+    c = HierPagedKVCache(num_players=2, num_groups=1, num_patches=4, num_local_hub_tokens=2,
+                         num_global_hub_tokens=2, num_heads=1, head_dim=8, local_attn_size=-1,
+                         num_frame_per_block=2, device="cpu", max_frames=4)
+    S = 2 * 2 * 4 + 2 * (1 * 2 + 2)
+    k = torch.zeros(S, 1, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="max_frames"):
+        c.append(k, k, 3, 2, np.ones((2, 1), bool))
+    with pytest.raises(ValueError, match="max_frames"):
+        c.append(k, k, 4, 2, np.ones((2, 1), bool))
+
+
+def test_cached_paths_refuse_autograd():
+    """The cached attention (paged pool) and the action branches' frame-window
+    attention are inference-only, like the reference's cached backends
+    (hier_paged_attention.py:123-124): with autograd on and parameters that
+    require grad they raise instead of silently detaching q/k/v."""
+    from multics_amd.action import frame_attention
+    from multics_amd.module import SelfAttention
+    attn = SelfAttention(64, 1)
+    attn.num_frame_per_block, attn.local_attn_size = 2, 4
+    c = HierPagedKVCache(num_players=2, num_groups=1, num_patches=4, num_local_hub_tokens=2,
+                         num_global_hub_tokens=2, num_heads=1, head_dim=64, local_attn_size=4,
+                         num_frame_per_block=2, device="cpu")
+    S = 2 * 2 * 4 + 2 * (2 + 2)
+    x = torch.zeros(1, S, 64)
+    freqs = torch.ones(S, 1, 32, dtype=torch.complex128)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        attn.causal_forward(x, freqs, kv_cache=c, num_frames=2, num_players=2,
+                            group_labels=torch.zeros(2, 2, dtype=torch.long))
+    q = torch.zeros(1, 3, 1, 64, requires_grad=True)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        frame_attention(q, q, q, torch.arange(3), torch.arange(3), 3, -1)

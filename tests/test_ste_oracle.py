@@ -72,3 +72,20 @@ def test_gate_index_classes():
     assert np.array_equal(gi[qi, ki], (t[qi] * N + g[ki]) * P + p[qi])
     qi, ki = np.nonzero(lp)
     assert np.array_equal(gi[qi, ki], (t[qi] * N + g[qi]) * P + p[ki])
+
+
+def test_row_sampled_gradient_equals_autograd():
+    """``ste_grad_at`` (only the gated rows, per bit) equals the autograd
+    logit gradient of the dense definition at every bit, including bits that
+    are off (no edges: zero) and inactive hub slots."""
+    from oracle.ste import ste_grad_at
+    for seed in (3, 4):
+        topo, logits, q, k, v, do = _case(seed)
+        lg = logits.clone().requires_grad_(True)
+        (ste_attention(q, k, v, topo, lg) * do).sum().backward()
+        T, N, P = logits.shape
+        bits = [(t, g, p) for t in range(T) for g in range(N) for p in range(P)]
+        got = ste_grad_at(q, k, v, do, topo, logits, bits)
+        want = lg.grad.reshape(-1).double().numpy()
+        assert np.allclose(got, want, atol=1e-5, rtol=1e-4), (got, want)
+        assert (np.abs(want) > 1e-4).sum() >= 4
