@@ -248,6 +248,16 @@ typedef struct HierBwdArgs {
 
 int hier_attn_bwd(const HierBwdArgs* args, void* stream);
 
+/* hier_attn_bwd without a caller workspace: no counterpart in the reference.  */
+/* For callers that cannot allocate device memory (code under HIP graph      */
+/* capture, tight training loops, harnesses that forbid hipMalloc).  Same    */
+/* arguments, kernels and results as hier_attn_bwd, except that delta and    */
+/* lse2 must be NULL: they live in a 16 MiB device array of the library      */
+/* (2 x H x lse_stride_h <= 4M floats, else HIER_EUNSUPPORTED), one copy per */
+/* GPU, held until the process ends and cleared by each call.  The call      */
+/* allocates nothing; calls that overlap on one GPU race on that array.      */
+int hier_attn_bwd_noalloc(const HierBwdArgs* args, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Paged KV cache append: copy the new K/V rows of a cached block into their */
 /* pool rows.  Replaces the per-stream rolling-cache writes and the per-call */

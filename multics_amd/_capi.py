@@ -111,6 +111,7 @@ EXPORTS = {
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],
+    "hier_attn_bwd_noalloc": [C.POINTER(HierBwdArgs), vp],
     "hier_kv_append": [C.POINTER(HierPageArgs), vp],
     "hier_frame_attn": [C.POINTER(HierFrameAttnArgs), vp],
     "hier_last_error": [],

@@ -32,6 +32,9 @@
 #include "hier_launch.h"
 #include "hier_tile.h"
 
+#include <algorithm>
+#include <mutex>
+
 namespace {
 
 using namespace hier::tile;
@@ -675,12 +678,9 @@ int64_t span_bytes(int64_t rows, int64_t ss, int64_t sh, int H, int D) {
   return ((rows > 0 ? rows - 1 : 0) * ss + (int64_t)(H - 1) * sh + D) * 2;
 }
 
-}  // namespace
-
-extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
-  hier::clear_error();
-  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
-  const HierBwdArgs& a = *args;
+// Argument checks and the launches of both entry points (a is complete: the
+// workspace pointers are set).
+int bwd_run(const HierBwdArgs& a, void* stream) {
   HIER_REQUIRE(a.D == 128 || a.D == 64, HIER_EUNSUPPORTED, "head_dim must be 64 or 128, got %d", a.D);
   HIER_REQUIRE(a.H >= 1 && a.n_items >= 0 && a.n_key_items >= 0 && a.kv_rows >= 0 && a.q_rows >= 0,
                HIER_EINVAL, "invalid H=%d n_items=%d n_key_items=%d", a.H, a.n_items, a.n_key_items);
@@ -750,4 +750,88 @@ extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
     return hier::check_launch("ste_kernel");
   }
   return HIER_OK;
+}
+
+// ---- workspace of the allocation-free entry point ---------------------------
+
+// delta and lse2 of hier_attn_bwd_noalloc: [H][lse_stride_h] floats each, in
+// this file-scope device array.  Each GPU the library runs on holds its own
+// copy until the process ends; every call on that GPU uses it, so calls that
+// overlap on one GPU (two streams, two threads) race.
+constexpr int64_t kScratchFloats = 4ll << 20;   // 16 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device.  The host-side symbol is
+// only a stand-in; the address comes from hipGetSymbolAddress, once per
+// device, with that device current.
+int scratch_ptr(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hier::fail(HIER_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  HIER_REQUIRE(dev >= 0 && dev < kMaxDevices, HIER_EUNSUPPORTED, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return hier::fail(HIER_ELAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return HIER_OK;
+}
+
+// Zero n floats (n % 4 == 0) with vector stores.  A kernel rather than
+// hipMemsetAsync so that the call stays correct inside captured graphs.
+__global__ void zero_kernel(float* p, int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  float4* q = reinterpret_cast<float4*>(p);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+    q[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+}  // namespace
+
+extern "C" int hier_attn_bwd(const HierBwdArgs* args, void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
+  return bwd_run(*args, stream);
+}
+
+extern "C" int hier_attn_bwd_noalloc(const HierBwdArgs* args, void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
+  HIER_REQUIRE(args->delta == nullptr && args->lse2 == nullptr, HIER_EINVAL,
+               "hier_attn_bwd_noalloc uses the library's device workspace: delta and lse2 must "
+               "be NULL");
+  HIER_REQUIRE(args->H >= 1 && args->lse_stride_h >= 0, HIER_EINVAL,
+               "invalid H=%d lse_stride_h=%lld", args->H, (long long)args->lse_stride_h);
+  // delta and lse2 each take H rows of lse_stride_h floats, rounded to 64
+  // floats so that lse2 starts 256-byte aligned
+  const int64_t per = ((int64_t)args->H * args->lse_stride_h + 63) / 64 * 64;
+  HIER_REQUIRE(2 * per <= kScratchFloats, HIER_EUNSUPPORTED,
+               "hier_attn_bwd_noalloc workspace holds 2 x H x lse_stride_h <= %lld floats (%lld "
+               "MiB); got H=%d x lse_stride_h=%lld",
+               (long long)kScratchFloats, (long long)(kScratchFloats * 4 >> 20), args->H,
+               (long long)args->lse_stride_h);
+  float* ws = nullptr;
+  int rc = scratch_ptr(&ws);
+  if (rc != HIER_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  // rows no item writes are read as 0, as from a zero-filled caller workspace
+  const int64_t n4 = 2 * per / 4;
+  if (n4 > 0) {
+    const int blocks = (int)std::min<int64_t>((n4 + 255) / 256, 2048);
+    hipLaunchKernelGGL(zero_kernel, dim3(blocks), dim3(256), 0, s, ws, n4);
+    rc = hier::check_launch("zero_kernel");
+    if (rc != HIER_OK) return rc;
+  }
+  HierBwdArgs a = *args;
+  a.delta = ws;
+  a.lse2 = ws + per;
+  return bwd_run(a, stream);
 }

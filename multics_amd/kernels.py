@@ -93,7 +93,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
                             dout: torch.Tensor, lse: torch.Tensor, tiles: TileList, *,
                             scale: Optional[float] = None,
                             key_tiles: Optional[TileList] = None,
-                            ste_geometry: Optional[tuple] = None):
+                            ste_geometry: Optional[tuple] = None,
+                            no_alloc_workspace: bool = False):
     """``hier_attn_bwd``: gradients ``(dq, dk, dv)`` (bf16, shaped like q/k/v) of
     ``hier_attention_forward(q, k, v, tiles)`` given its output, its ``lse``
     and the output gradient.  ``tiles`` must be a full-sequence tile list;
@@ -102,6 +103,10 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     With ``ste_geometry=(P, T, L, N, KL)`` a fourth result is returned: the
     sum of dS = P (dP - delta) over the membership-gated edges of every bit,
     as an fp32 ``[T, N, P]`` tensor (see ``membership_grad``).
+
+    ``no_alloc_workspace=True`` calls ``hier_attn_bwd_noalloc``, whose
+    per-row workspace lives in the library's device array instead of a
+    tensor allocated here (same results; 2 x H x rows <= 4M floats).
     """
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
         if t.dtype != torch.bfloat16:
@@ -131,7 +136,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     dq = torch.zeros_like(q3)
     dk = torch.zeros_like(k3)
     dv = torch.zeros_like(v3)
-    ws = torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
+    ws = None if no_alloc_workspace else \
+        torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
     ste = None
     if ste_geometry is not None:
         P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
@@ -144,7 +150,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
         kv_rows=min(k3.shape[0], v3.shape[0]), q_rows=min(q3.shape[0], d3.shape[0]), reserved=0,
         q=q3.data_ptr(), k=k3.data_ptr(), v=v3.data_ptr(), o=o3.data_ptr(), dout=d3.data_ptr(),
-        lse=lse.data_ptr(), delta=ws[0].data_ptr(), lse2=ws[1].data_ptr(),
+        lse=lse.data_ptr(), delta=None if ws is None else ws[0].data_ptr(),
+        lse2=None if ws is None else ws[1].data_ptr(),
         dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(),
         q_ss=q_ss, q_sh=q_sh, k_ss=k_ss, k_sh=k_sh, v_ss=v_ss, v_sh=v_sh, o_ss=o_ss, o_sh=o_sh,
         do_ss=do_ss, do_sh=do_sh, dq_ss=dq.stride(0), dq_sh=dq.stride(1), dk_ss=dk.stride(0),
@@ -159,7 +166,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         args.ste_items, args.ste_kv_idx = sl.items.data_ptr(), sl.kv_idx.data_ptr()
         args.ste_kv_mask, args.ste_kv_class = sl.kv_mask.data_ptr(), scls.data_ptr()
         args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
-    _capi.call("hier_attn_bwd", C.byref(args), _stream(dev))
+    _capi.call("hier_attn_bwd_noalloc" if no_alloc_workspace else "hier_attn_bwd", C.byref(args),
+               _stream(dev))
     shape = lambda g, like: g.reshape(like.shape) if like.dim() == 4 else g
     res = (shape(dq, q), shape(dk, k), shape(dv, v))
     if ste_geometry is None:
