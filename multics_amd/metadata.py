@@ -917,3 +917,88 @@ def clear_hier_tiled_layout_cache() -> None:
 
 def clear_metadata_cache() -> None:
     _META_CACHE.clear()
+
+
+# --------------------------------------------------------------------------
+# packed varlen plan
+# --------------------------------------------------------------------------
+
+_PLAN_CACHE: "OrderedDict[tuple, dict]" = OrderedDict()
+
+
+def _get_varlen_plan(*, kv_index, kv_count, qbase, qlen, seg_ids, query_tokens):
+    """The packed-varlen plan of ``_build_metadata`` arrays built with one
+    program per segment (hier_packed_attention.py:32-102): same keys, dtypes
+    and errors.  The segments must partition the query rows
+    ``[0, query_tokens)`` exactly (``AssertionError`` otherwise); active
+    segments (rows and keys both non-empty) are flattened into ``q_index`` /
+    ``k_index`` (int64) with int32 offsets ``cu_q`` / ``cu_k``.  The flattening
+    runs as device gathers (no per-row host loop); the plan is cached by the
+    source tensors' data pointers and keeps references to them, so a reused
+    allocation cannot alias a stale plan (WAN_HIER_PACKED_PLAN_CACHE_SIZE,
+    default 64, as the reference)."""
+    dev = kv_index.device
+    key = (str(dev), kv_index.data_ptr(), kv_count.data_ptr(), qbase.data_ptr(), qlen.data_ptr(),
+           seg_ids.data_ptr(), int(query_tokens))
+    hit = _lru_get(_PLAN_CACHE, key)
+    if hit is not None:
+        return hit
+    qb = qbase.detach().to("cpu", torch.int64).numpy()
+    qn = qlen.detach().to("cpu", torch.int64).numpy()
+    si = seg_ids.detach().to("cpu", torch.int64).numpy()
+    nk = kv_count.detach().to("cpu", torch.int64).numpy()
+    if not np.array_equal(si, np.arange(len(si))):
+        raise AssertionError("packed metadata must contain exactly one program per segment")
+    # an exact partition in program order: every non-empty program starts
+    # where the previous one ended, the first at 0, the last ends at
+    # query_tokens (empty programs cover nothing)
+    pos, ok = 0, True
+    for b, n in zip(qb.tolist(), qn.tolist()):
+        if n <= 0:
+            continue
+        if b != pos:
+            ok = False
+            break
+        pos += n
+    if not ok or pos != int(query_tokens):
+        raise AssertionError("packed query segments must partition the query sequence exactly")
+    act = np.nonzero((qn > 0) & (nk[si] > 0))[0]
+    qa, ka = qn[act], nk[si[act]]
+    cu_q = np.concatenate([[0], np.cumsum(qa)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(ka)]).astype(np.int32)
+    # rows: starts repeated per row plus the position inside the segment
+    rows_dev = torch.arange(int(cu_q[-1]), device=dev, dtype=torch.int64)
+    seg_of_row = torch.repeat_interleave(torch.arange(len(act), device=dev),
+                                         torch.from_numpy(qa).to(dev)) if len(act) else rows_dev
+    cuq_dev = torch.from_numpy(cu_q.astype(np.int64)).to(dev)
+    qb_act = torch.from_numpy(qb[act]).to(dev)
+    q_flat = (qb_act[seg_of_row] + rows_dev - cuq_dev[seg_of_row]) if len(act) else rows_dev
+    # keys: the first count entries of each active segment's row of kv_index
+    if len(act):
+        width = kv_index.shape[1]
+        kpos = torch.arange(int(cu_k[-1]), device=dev, dtype=torch.int64)
+        seg_of_key = torch.repeat_interleave(torch.arange(len(act), device=dev),
+                                             torch.from_numpy(ka).to(dev))
+        cuk_dev = torch.from_numpy(cu_k.astype(np.int64)).to(dev)
+        sid_act = torch.from_numpy(si[act]).to(dev)
+        flat = sid_act[seg_of_key] * width + (kpos - cuk_dev[seg_of_key])
+        k_flat = kv_index.reshape(-1)[flat].to(torch.int64)
+    else:
+        k_flat = torch.empty(0, device=dev, dtype=torch.int64)
+    res = {
+        "q_index": q_flat,
+        "k_index": k_flat,
+        "cu_q": torch.from_numpy(cu_q).to(dev),
+        "cu_k": torch.from_numpy(cu_k).to(dev),
+        "max_q": int(qa.max()) if len(act) else 0,
+        "max_k": int(ka.max()) if len(act) else 0,
+        "min_k_index": int(k_flat.min().item()) if k_flat.numel() else 0,
+        "max_k_index": int(k_flat.max().item()) if k_flat.numel() else -1,
+        "metadata_sources": (kv_index, kv_count, qbase, qlen, seg_ids),
+    }
+    _lru_put(_PLAN_CACHE, key, res, "WAN_HIER_PACKED_PLAN_CACHE_SIZE", "64")
+    return res
+
+
+def clear_varlen_plan_cache() -> None:
+    _PLAN_CACHE.clear()

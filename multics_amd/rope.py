@@ -23,8 +23,8 @@ WAN_REROPE_SPLITS = (12, 32, 42, 42)   # rope.py:5
 
 def precompute_freqs_cis(dim: int, end: int = 1024, theta: float = 10000.0) -> torch.Tensor:
     """``exp(i * t * theta^(-2j/dim))`` for t < end, j < dim/2, complex128 (rope.py:103-107)."""
-    inv = theta ** (-(torch.arange(0, dim, 2)[: dim // 2].double() / dim))
-    ang = torch.arange(end, dtype=torch.float64)[:, None] * inv[None, :]
+    inv = 1.0 / theta ** (torch.arange(0, dim, 2)[: dim // 2].double() / dim)
+    ang = torch.outer(torch.arange(end, dtype=torch.float64), inv)
     return torch.polar(torch.ones_like(ang), ang)
 
 

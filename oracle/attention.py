@@ -18,13 +18,26 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 * ``camera_to_world``, ``camera12`` -- data/raw_inputs.py:250-273,
   data/dataset.py:49-90.
 
-Parity pins: masked attention is the textbook softmax(QK^T/sqrt(D)) V with the
-dense mask of ``oracle.masks`` (itself pinned against the reference's tests and
-golden layouts), cross-checked against an independent per-row numpy loop on
-small shapes; ``attention_grads_at`` against torch autograd through
-``masked_attention`` on small shapes; RMSNorm/RoPE/freqs against closed forms and the simplex
-invariants of tests/test_simplex_rope.py:21-54; camera12 against the rigid
-transform identities (anchor frame maps to the identity pose).
+Parity pins (tests/test_oracle_rope_camera.py, tests/test_oracle_grads.py):
+* ``masked_attention`` -- against torch's ``scaled_dot_product_attention`` with
+  the dense mask of ``oracle.masks`` (itself pinned against the reference's
+  tests and golden layouts) on every live row; inactive local-hub rows 0.
+* ``attention_grads_at`` -- against torch autograd through
+  ``masked_attention`` on small shapes.
+* ``precompute_freqs_cis`` / ``rerope_bands`` -- closed-form angles, unit
+  modulus and the group law; the temporal band is the lowest six frequencies
+  of the 44-channel Wan band.
+* ``simplex_vertices`` -- the invariants of tests/test_simplex_rope.py:21-32
+  (unit norm, squared distance 2m/(m-1)), centring and the m = 2 closed form.
+* ``player_freqs`` / ``hub_freqs`` -- agent-band constancy and per-player
+  difference (tests/test_simplex_rope.py:35-54) and per-band indexing.
+* ``camera_to_world`` / ``camera12`` -- rigid-transform identities (proper
+  rotations, anchor -> [I | 0], invariance under a global rigid motion,
+  1/pos_scale translation, composition).
+* ``rms_norm`` / ``camera_qk`` / ``rope_apply`` / ``project_qk`` -- the fused
+  HIP prologue matches them on > 99 % of elements bit for bit (the rest
+  1 ulp), and the module's autograd path (torch ops in the reference's order)
+  matches them through the module tests.
 """
 
 from __future__ import annotations

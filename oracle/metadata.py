@@ -25,9 +25,10 @@ Parity pins:
 * the Tiled128 arrays are checked against golden vectors written by the
   reference's own layout builders, and their logical edges against the dense
   mask (``oracle.masks``) as in ``tests/test_hier_tiled_layout.py:30-95``;
-* the varlen plan is checked against its own invariants (queries partitioned
-  exactly, ``cu_*`` monotone and consistent) -- its arrays are a pure
-  flattening of the segmented lists.
+* the varlen plan is built from the reference's own golden segmented lists
+  and checked by brute force: its (query, key) pairs are exactly the lists'
+  pairs, their count is the reference's ``logical_pairs``, and the refusal
+  cases raise (``tests/test_varlen_plan.py``).
 """
 
 from __future__ import annotations
