@@ -19,53 +19,11 @@ import torch
 
 from . import _capi
 from .module import rope_apply
+from .rolling import rolling_cache_append  # noqa: F401  (re-exported)
 
 
 def _stream(dev) -> C.c_void_p:
     return C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-
-
-def rolling_cache_append(kv_cache: dict, roped_key: torch.Tensor, value: torch.Tensor,
-                         current_start: int, current_end: int, local_attn_size: int,
-                         sink_size: int, tokens_per_frame: int):
-    """attention.py:90-163: write tokens [current_start, current_end) into a
-    rolling cache.  Tokens already cached are refreshed in place; new ones
-    are appended, and when the buffer overflows (windowed caches) the oldest
-    non-sink tokens are dropped by moving the rest towards the front.
-    Returns ``(attn_start, local_end)``, the buffer range the new tokens
-    attend to."""
-    sink = sink_size * tokens_per_frame
-    size = kv_cache["k"].shape[1]
-    g_end = int(kv_cache["global_end_index"].item())
-    l_end = int(kv_cache["local_end_index"].item())
-    n_new = min(roped_key.shape[1], max(0, current_end - g_end))
-    if n_new == 0 and l_end > 0:           # a re-run block: refresh what is cached
-        g_start = g_end - l_end
-        r0, r1 = max(current_start, g_start), min(current_end, g_end)
-        if r1 > r0:
-            src, dst = r0 - current_start, r0 - g_start
-            kv_cache["k"][:, dst:dst + r1 - r0] = roped_key[:, src:src + r1 - r0]
-            kv_cache["v"][:, dst:dst + r1 - r0] = value[:, src:src + r1 - r0]
-    new_end = l_end + n_new
-    if local_attn_size != -1 and current_end > g_end and new_end > size:
-        evict = max(0, min(new_end - size, new_end - sink - 1))
-        if evict > 0:
-            keep = max(0, l_end - evict - sink)
-            if keep > 0:
-                for name in ("k", "v"):
-                    kv_cache[name][:, sink:sink + keep] = \
-                        kv_cache[name][:, sink + evict:sink + evict + keep].clone()
-            new_end = min(l_end + n_new - evict, size)
-    if n_new > 0:
-        kv_cache["k"][:, new_end - n_new:new_end] = roped_key[:, -n_new:]
-        kv_cache["v"][:, new_end - n_new:new_end] = value[:, -n_new:]
-    max_attn = size if local_attn_size == -1 else min(local_attn_size * tokens_per_frame, size)
-    attn_start = max(0, new_end - max_attn)
-    if sink_size > 0 and sink > attn_start:
-        attn_start = 0
-    kv_cache["global_end_index"].fill_(current_end)
-    kv_cache["local_end_index"].fill_(new_end)
-    return attn_start, new_end
 
 
 def ensure_action_cache(parent: dict, name: str, batch: int, n_heads: int, head_dim: int,

@@ -890,6 +890,32 @@ def cached_tiles(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn, fram
     return hit
 
 
+def cached_stream_tiles(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn,
+                        agent_frame_lists, local_frame_lists, global_frame_list,
+                        local_active_frames, labels, q_active, direct_player, tile_bases,
+                        membership=None, global_only=None, hier_no_local_hub=False) -> TileList:
+    """Tile list of one cached call over per-stream frame lists (the
+    ``_build_metadata`` inputs) whose K/V rows sit at ``tile_bases`` = (agent
+    [P][i], local [N][i], global [i]): the first row of cached frame i of each
+    stream in one K/V pool.  Cached in the segmented-metadata LRU."""
+    no_local = bool(hier_no_local_hub)
+    key = ("streams", str(torch.device(device)), P, N, L, KL, KG, n_frames, n_block, local_attn,
+           _freeze(agent_frame_lists), _freeze(local_frame_lists), _freeze(global_frame_list),
+           _freeze(tile_bases), _freeze(local_active_frames), _freeze(labels), _freeze(q_active),
+           bool(direct_player), no_local, _freeze(membership), _freeze(global_only))
+    hit = _lru_get(_META_CACHE, key)
+    if hit is None:
+        topo = cached_topology(
+            P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n_frames, n_block=n_block, local_attn=local_attn,
+            agent_frame_lists=agent_frame_lists, local_frame_lists=local_frame_lists,
+            global_frame_list=global_frame_list, local_active_frames=local_active_frames,
+            labels=labels, q_active=q_active, direct_player=direct_player, membership=membership,
+            global_only=global_only, hier_no_local_hub=no_local, tile_bases=tile_bases)
+        hit = build(topo, device).tiles
+        _lru_put(_META_CACHE, key, hit, "WAN_HIER_SEGMENTED_META_CACHE_SIZE", "64")
+    return hit
+
+
 def build_hier_tiled_cached_layout(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn,
                                    agent_frame_lists, local_frame_lists, global_frame_list,
                                    local_active_frames, labels, q_active, direct_player):

@@ -35,7 +35,10 @@ import torch.nn.functional as F
 
 from . import metadata as M
 from .kernels import hier_attention, hier_attention_forward, qkv_prologue
+from .hier_masks import HierBlockMask
+from .kv_cache import stream_pool
 from .paged_cache import HierPagedKVCache
+from .rolling import rolling_bool_cache_append, rolling_cache_append
 from .rope import freqs_to_cos_sin
 from .topology import _prepare_hier_group_tensors, _prepare_hier_membership_tensors
 
@@ -244,11 +247,16 @@ class SelfAttention(nn.Module):
         return self._hier(x, freqs, tiles, cam_tokens, logits=membership_logits, geometry=geometry)
 
     def forward(self, x, freqs, mask=None, cam_tokens=None):
-        """attention.py:436-442 for dense boolean (or no) masks."""
+        """attention.py:436-442.  ``mask`` is a ``hier_masks.HierBlockMask``
+        (the drop-in for the reference's FlexAttention BlockMask of the
+        hierarchical topology: HIP forward, and HIP backward under autograd),
+        a dense boolean mask or None (``scaled_dot_product_attention``)."""
+        if isinstance(mask, HierBlockMask):
+            return self._forward_block_mask(x, freqs, mask, cam_tokens)
         if mask is not None and not torch.is_tensor(mask):
             raise NotImplementedError(
-                "FlexAttention BlockMask masks are not available in this build; hierarchical "
-                "topologies use forward_hier_tiled_ste / forward_hier_membership")
+                f"unsupported mask type {type(mask).__name__}: pass the HierBlockMask of "
+                "multics_amd.hier_masks.build_stage2_hier_flex_block_mask, a dense bool mask or None")
         q, k, v = self._project_self_attn_qkv(x, freqs, cam_tokens)
         b, s, _ = q.shape
         H = self.num_heads
@@ -256,6 +264,31 @@ class SelfAttention(nn.Module):
         am = None if mask is None else mask.to(device=q.device, dtype=torch.bool)
         y = F.scaled_dot_product_attention(split(q), split(k), split(v), attn_mask=am)
         return self.o(y.transpose(1, 2).reshape(b, s, self.dim))
+
+    def _forward_block_mask(self, x, freqs, mask, cam_tokens):
+        """The FlexAttention path (attention.py:322-353, 436-442) on the HIP
+        kernels.  Every edge of the mask except one class is in the tile list;
+        the exception, an inactive local-hub row's self edge, is a softmax over
+        one key, so that row's output is its own value (and its query and key
+        get no gradient from it)."""
+        b, s, dim = x.shape
+        if b != 1:
+            raise NotImplementedError("hierarchical attention supports B=1")
+        if s != mask.S:
+            raise ValueError(f"x has {s} tokens, the block mask covers S={mask.S}")
+        H, D = self.num_heads, self.head_dim
+        if torch.is_grad_enabled():
+            q, k, v = (t.to(torch.bfloat16).view(s, H, D)
+                       for t in self._project_self_attn_qkv(x, freqs, cam_tokens))
+            y = hier_attention(q, k, v, mask.tiles)
+        else:
+            q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
+            y = torch.zeros((s, H, D), dtype=torch.bfloat16, device=x.device)
+            hier_attention_forward(q, k, v, mask.tiles, y)
+        if mask.self_rows.numel():
+            rows = mask.self_rows.to(x.device)
+            y = y.index_copy(0, rows, v.index_select(0, rows).to(y.dtype))
+        return self.o(y.reshape(1, s, dim).to(self.o.weight.dtype))
 
     # ---- cached rollout (attention.py:456-1043) ------------------------------------
 
@@ -272,9 +305,10 @@ class SelfAttention(nn.Module):
         negative prompts of classifier-free guidance, which the reference runs
         as two calls on two caches): the members share the topology and run
         in one attention launch."""
-        if not isinstance(kv_cache, HierPagedKVCache):
-            raise NotImplementedError("cached hierarchical attention runs on a "
-                                      "paged_cache.HierPagedKVCache")
+        paged = isinstance(kv_cache, HierPagedKVCache)
+        if not paged and not (isinstance(kv_cache, dict) and kv_cache.get("hier_hub", False)):
+            raise ValueError("Hierarchical causal attention requires a hier KV cache "
+                             "(a paged_cache.HierPagedKVCache or the reference's cache dict)")
         if torch.is_grad_enabled() and (x.requires_grad or
                                         any(p.requires_grad for p in self.parameters())):
             # the reference's cached backends refuse autograd the same way
@@ -284,9 +318,10 @@ class SelfAttention(nn.Module):
                                "enabled and the input or the weights require grad); run it "
                                "under torch.no_grad() or torch.inference_mode()")
         b, s, dim = x.shape
-        if b != kv_cache.B:
-            raise NotImplementedError("hierarchical attention supports B=1" if kv_cache.B == 1 else
-                                      f"the KV cache holds a batch of {kv_cache.B}, got B={b}")
+        cache_b = kv_cache.B if paged else 1
+        if b != cache_b:
+            raise NotImplementedError("hierarchical attention supports B=1" if cache_b == 1 else
+                                      f"the KV cache holds a batch of {cache_b}, got B={b}")
         H, D = self.num_heads, self.head_dim
         P = int(num_players if num_players is not None else kv_cache["num_players"])
         N, KL, KG = int(kv_cache["num_groups"]), int(kv_cache["num_local_hub_tokens"]), \
@@ -294,7 +329,7 @@ class SelfAttention(nn.Module):
         no_local = bool(getattr(self, "hier_no_local_hub", False))
         if bool(kv_cache.get("hier_no_local_hub", False)) != no_local:
             raise ValueError("hier_no_local_hub mismatch between SelfAttention and KV cache")
-        if P != kv_cache.P:
+        if paged and P != kv_cache.P:
             raise ValueError(f"num_players={P} does not match the KV cache ({kv_cache.P})")
         n = int(num_frames)
         k_total = int(num_hub_tokens if num_hub_tokens is not None else N * KL + KG)
@@ -319,7 +354,7 @@ class SelfAttention(nn.Module):
             raise ValueError(f"hier_hub causal seq shape invalid: S={s}, hub_len={hub_len}, P={P}, "
                              f"n={n}")
         L = agent_len // (P * n)
-        if L != kv_cache.L:
+        if paged and L != kv_cache.L:
             raise ValueError(f"tokens per player frame {L} do not match the KV cache ({kv_cache.L})")
         if freqs.shape[0] != s:
             raise ValueError("hier_hub causal_forward expects freqs.shape[0] == seq_len")
@@ -336,6 +371,12 @@ class SelfAttention(nn.Module):
                 raise ValueError("hier_hub cached inference requires membership / global_only "
                                  "constant inside each latent block")
             act = act[start_frame:start_frame + n]
+        if not paged:
+            return self._causal_rolling(
+                x, freqs, kv_cache, start_frame=start_frame, n=n, P=P, N=N, L=L, KL=KL, KG=KG,
+                labels=labels, act=act, mem=mem if use_mem else None,
+                go=go if use_mem else None, no_local=no_local, direct_player=direct_player,
+                cam_tokens=cam_tokens)
         if b == 1:
             q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
         else:   # batch-major heads: member i's head h is head i * H + h
@@ -358,6 +399,94 @@ class SelfAttention(nn.Module):
         hier_attention_forward(q, kv_cache.k, kv_cache.v, tiles, out)
         out = out.view(s, b, dim).transpose(0, 1)
         return self.o(out.to(self.o.weight.dtype))
+
+    def _causal_rolling(self, x, freqs, kv_cache, *, start_frame, n, P, N, L, KL, KG, labels,
+                        act, mem, go, no_local, direct_player, cam_tokens):
+        """One cached block over the reference's cache dict: the block's K/V are
+        appended to every stream's rolling buffer (attention.py:605-666,
+        rolling.py), the windows are read where they lie -- in place when the
+        buffers are slices of one pool (``kv_cache.initialize_hier_kv_cache``),
+        else concatenated as the reference's backends do -- and one HIP
+        forward computes every stream."""
+        s, dim = x.shape[1], x.shape[2]
+        H, D = self.num_heads, self.head_dim
+        dev = x.device
+        W = int(self.local_attn_size)
+        retention = W + n if W != -1 else -1
+        q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
+        a_len = P * n * L
+        l0, g0 = a_len, a_len + n * N * KL
+        agents, hubs, glob = kv_cache["agent_caches"], kv_cache["local_hubs"], kv_cache["global_hub"]
+        f0, f1 = start_frame, start_frame + n
+        ka, va = k[:a_len].reshape(P, n * L, H, D), v[:a_len].reshape(P, n * L, H, D)
+        for p in range(P):
+            rolling_cache_append(agents[p], ka[p][None], va[p][None], f0 * L, f1 * L, retention, 0, L)
+        if not no_local:
+            kl, vl = k[l0:g0].reshape(n, N, KL, H, D), v[l0:g0].reshape(n, N, KL, H, D)
+            act_dev = act.to(dev)
+            for g in range(N):
+                rolling_bool_cache_append(hubs[g], "active", act_dev[:, g].repeat_interleave(KL),
+                                          f0 * KL, f1 * KL, retention, 0, KL)
+                rolling_cache_append(hubs[g], kl[:, g].reshape(1, n * KL, H, D),
+                                     vl[:, g].reshape(1, n * KL, H, D), f0 * KL, f1 * KL,
+                                     retention, 0, KL)
+        if KG > 0:
+            rolling_cache_append(glob, k[g0:].reshape(1, n * KG, H, D),
+                                 v[g0:].reshape(1, n * KG, H, D), f0 * KG, f1 * KG, retention, 0,
+                                 KG)
+        end_frame = f1 - 1
+
+        def window(c, tpf):          # attention.py:667-674
+            local_end = int(c["local_end_index"].item())
+            n_cached = local_end // tpf if tpf > 0 else 0
+            first = end_frame - n_cached + 1
+            return list(range(first, first + n_cached)), local_end
+
+        streams = [(c, L) for c in agents]
+        if not no_local:
+            streams += [(c, KL) for c in hubs]
+        if KG > 0:
+            streams += [(glob, KG)]
+        wins = [window(c, tpf) for c, tpf in streams]
+        pool = stream_pool(kv_cache)
+        if pool is not None and (no_local or len(hubs) == N):
+            pk, pv, offs = pool
+            offs = list(offs[:P + (0 if no_local else N)]) + [offs[-1]]
+            kpool, vpool = pk[0], pv[0]
+        else:                        # buffers outside one pool: concatenate the windows
+            kpool = torch.cat([c["k"][0, :e] for (c, _), (_, e) in zip(streams, wins)], dim=0)
+            vpool = torch.cat([c["v"][0, :e] for (c, _), (_, e) in zip(streams, wins)], dim=0)
+            offs, o = [], 0
+            for _, e in wins:
+                offs.append(o)
+                o += e
+            if KG == 0:
+                offs.append(o)
+        base = lambda i, tpf: [offs[i] + j * tpf for j in range(len(wins[i][0]))]
+        agent_b = [base(p, L) for p in range(P)]
+        local_b = [] if no_local else [base(P + g, KL) for g in range(N)]
+        gi = P + (0 if no_local else N)
+        glob_b = base(gi, KG) if KG > 0 else []
+        lact = []
+        if not no_local:
+            for g in range(N):
+                nf = len(wins[P + g][0])
+                a = hubs[g]["active"][:nf * KL].reshape(nf, KL).any(dim=1).tolist() \
+                    if KL > 0 else [True] * nf
+                lact.append([bool(x_) for x_ in a])
+        tiles = M.cached_stream_tiles(
+            device=dev, P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n,
+            n_block=int(self.num_frame_per_block), local_attn=W,
+            agent_frame_lists=[wins[p][0] for p in range(P)],
+            local_frame_lists=[] if no_local else [wins[P + g][0] for g in range(N)],
+            global_frame_list=wins[gi][0] if KG > 0 else [], local_active_frames=lact,
+            labels=None if labels is None else labels.tolist(), q_active=act.tolist(),
+            direct_player=bool(direct_player), tile_bases=(agent_b, local_b, glob_b),
+            membership=None if mem is None else mem.numpy(),
+            global_only=None if go is None else go.numpy(), hier_no_local_hub=no_local)
+        out = torch.zeros((s, H, D), dtype=torch.bfloat16, device=dev)
+        hier_attention_forward(q, kpool, vpool, tiles, out)
+        return self.o(out.view(1, s, dim).to(self.o.weight.dtype))
 
     def causal_forward(self, x, freqs, mask=None, grid_sizes=None, seq_lens=None, kv_cache=None,
                        current_start=0, cache_start=None, num_frames=None, num_players=None,

@@ -38,5 +38,5 @@ def expand_tiles(tiles):
 
 
 def err_stats(actual: torch.Tensor, expected: torch.Tensor):
-    d = (actual.float().cpu() - expected.float().cpu()).abs()
+    d = (actual.detach().float().cpu() - expected.detach().float().cpu()).abs()
     return float(d.max()), float(d.mean())

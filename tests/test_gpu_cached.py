@@ -12,6 +12,8 @@ from multics_amd.kernels import (
     hierarchical_paged_kv_attention,
     hierarchical_segmented_attention,
 )
+from multics_amd.kv_cache import (HierKVCachePipelineMixin, initialize_hier_kv_cache,
+                                  stream_pool)
 from multics_amd.module import SelfAttention
 from multics_amd.paged_cache import HierPagedKVCache
 from oracle.cached import HierCacheState, cached_block_forward
@@ -57,17 +59,42 @@ CASES = [
 ]
 
 
+def _cache(store, P, N, L, KL, KG, H, D, W, n):
+    """A layer's KV cache: the paged pool, the reference's cache dict over one
+    pool (``kv_cache.initialize_hier_kv_cache``), or that dict with every
+    stream buffer replaced by its own tensor, as the reference allocates them
+    (read by concatenation)."""
+    if store == "paged":
+        return HierPagedKVCache(num_players=P, num_groups=N, num_patches=L,
+                                num_local_hub_tokens=KL, num_global_hub_tokens=KG, num_heads=H,
+                                head_dim=D, local_attn_size=W, num_frame_per_block=n,
+                                device="cuda")
+    entry = initialize_hier_kv_cache(
+        num_layers=1, batch_size=1, dtype=torch.bfloat16, device="cuda", num_players=P,
+        num_groups=N, num_local_hub_tokens=KL, num_global_hub_tokens=KG, frame_seq_length=L,
+        local_attn_size=W, num_frame_per_block=n, num_heads=H, head_dim=D)[0]
+    if store == "separate_dict":
+        for c in list(entry["agent_caches"]) + list(entry["local_hubs"]) + [entry["global_hub"]]:
+            c["k"], c["v"] = torch.zeros_like(c["k"]), torch.zeros_like(c["v"])
+        assert stream_pool(entry) is None
+    else:
+        assert stream_pool(entry) is not None
+    return entry
+
+
+STORES = ["paged", "pooled_dict", "separate_dict"]
+
+
+@pytest.mark.parametrize("store", STORES)
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_module_rollout_matches_cached_oracle(case):
+def test_module_rollout_matches_cached_oracle(case, store):
     need_gpu()
     name, P, T, L, N, KL, KG, n, W, H, D, direct, kind = case
     dim = H * D
     m = _module(dim, H, seed=1)
     m.num_frame_per_block, m.local_attn_size = n, W
     rng = np.random.default_rng(2)
-    cache = HierPagedKVCache(num_players=P, num_groups=N, num_patches=L, num_local_hub_tokens=KL,
-                             num_global_hub_tokens=KG, num_heads=H, head_dim=D, local_attn_size=W,
-                             num_frame_per_block=n, device="cuda")
+    cache = _cache(store, P, N, L, KL, KG, H, D, W, n)
     st = HierCacheState(P, N, L, KL, KG, H, D, W, n)
     if kind == "membership":
         mem = np.zeros((T, N, P), bool)
@@ -94,7 +121,7 @@ def test_module_rollout_matches_cached_oracle(case):
         freqs = torch.polar(torch.ones_like(ang), ang)
         for step in range(2):       # two denoising passes over the block, then the next block
             x = torch.randn(1, S, dim, generator=g).to("cuda", torch.bfloat16)
-            say(f"rollout {name} block {b} step {step}")
+            say(f"rollout {name} ({store}) block {b} step {step}")
             with torch.no_grad():
                 y = m.causal_forward(x, freqs, kv_cache=cache, current_start=b * n * P * L,
                                      num_frames=n, num_players=P, **kw)
@@ -207,3 +234,93 @@ def test_cfg_batch_cache_matches_two_caches():
         o = torch.zeros(S, H, D, dtype=torch.bfloat16, device="cuda")
         hier_attention_forward(q2[:, i * H:(i + 1) * H].contiguous(), c.k, c.v, tiles, o)
         assert torch.equal(out2[:, i * H:(i + 1) * H], o)
+
+
+def _rollout(m, cache, P, T, L, N, KL, KG, n, H, D, seed, passes=2):
+    """Outputs of every (block, pass) of a labels rollout through ``cache``."""
+    rng = np.random.default_rng(seed)
+    g = torch.Generator().manual_seed(seed)
+    S = P * n * L + n * (N * KL + KG)
+    outs = []
+    for b in range(T // n):
+        lab = np.repeat(rng.integers(0, N, size=(1, P)), n, axis=0)
+        act = np.zeros((n, N), bool)
+        act[np.arange(n)[:, None], lab] = True
+        ang = torch.rand(S, 1, D // 2, generator=g, dtype=torch.float64) * 6.283
+        freqs = torch.polar(torch.ones_like(ang), ang)
+        for _ in range(passes):
+            x = torch.randn(1, S, H * D, generator=g).to("cuda", torch.bfloat16)
+            with torch.inference_mode():
+                outs.append(m.causal_forward(
+                    x, freqs, kv_cache=cache, current_start=b * n * P * L, num_frames=n,
+                    num_players=P, num_hub_tokens=N * KL + KG, group_labels=torch.from_numpy(lab),
+                    active_group=torch.from_numpy(act), direct_player=True))
+    torch.cuda.synchronize()
+    return outs
+
+
+def test_pooled_and_separate_dicts_agree_bit_for_bit():
+    """The same rolling-buffer contents read in place from the pool or
+    concatenated from separate tensors give identical outputs."""
+    need_gpu()
+    P, T, L, N, KL, KG, n, W, H, D = 4, 12, 20, 2, 5, 6, 3, 3, 2, 128
+    m = _module(H * D, H, seed=4)
+    m.num_frame_per_block, m.local_attn_size = n, W
+    say("pooled vs separate cache dicts")
+    a = _rollout(m, _cache("pooled_dict", P, N, L, KL, KG, H, D, W, n), P, T, L, N, KL, KG, n,
+                 H, D, seed=9)
+    b = _rollout(m, _cache("separate_dict", P, N, L, KL, KG, H, D, W, n), P, T, L, N, KL, KG, n,
+                 H, D, seed=9)
+    for i, (x, y) in enumerate(zip(a, b)):
+        assert torch.equal(x, y), i
+
+
+class _Blocks:
+    def __init__(self, attn):
+        self.self_attn = attn
+
+
+class _Dit:
+    def __init__(self, attn, N, KL, KG):
+        self.blocks = [_Blocks(attn)]
+        self.num_groups, self.num_local_hub_tokens, self.num_global_hub_tokens = N, KL, KG
+        self.hier_no_local_hub = False
+
+
+class _Pipe(HierKVCachePipelineMixin):
+    """The attributes of WanVideoNPlayersPipeline that its cache methods read."""
+
+    def __init__(self, attn, P, N, L, KL, KG, W, n):
+        self.dit = _Dit(attn, N, KL, KG)
+        self.num_players, self.frame_seq_length = P, L
+        self.local_attn_size, self.num_frame_per_block = W, n
+        self.num_transformer_blocks = 2
+        self.torch_dtype = torch.bfloat16
+        self.kv_cache1 = None
+        self.crossattn_cache = None
+
+    def _initialize_crossattn_cache(self, batch_size, dtype, device):
+        self.crossattn_cache = [{"is_init": True} for _ in range(self.num_transformer_blocks)]
+
+
+def test_pipeline_cache_methods_reset_and_reuse():
+    """The drop-in pipeline methods: allocate for training, roll out, reset
+    through init_kv_cache_for_training (detach + _reset_kv_cache), roll out
+    again -- the second rollout equals the first bit for bit."""
+    need_gpu()
+    P, T, L, N, KL, KG, n, W, H, D = 3, 9, 16, 2, 2, 3, 3, 3, 2, 64
+    m = _module(H * D, H, seed=5)
+    m.num_frame_per_block, m.local_attn_size = n, W
+    pipe = _Pipe(m, P, N, L, KL, KG, W, n)
+    pipe.init_kv_cache_for_training(batch_size=P, device=torch.device("cuda"))
+    assert len(pipe.kv_cache1) == 2 and pipe.crossattn_cache is not None
+    say("pipeline cache methods: first rollout")
+    first = _rollout(m, pipe.kv_cache1[0], P, T, L, N, KL, KG, n, H, D, seed=12)
+    pipe.init_kv_cache_for_training(batch_size=P, device=torch.device("cuda"))
+    assert all(not c["is_init"] for c in pipe.crossattn_cache)
+    assert int(pipe.kv_cache1[0]["agent_caches"][0]["local_end_index"].item()) == 0
+    assert stream_pool(pipe.kv_cache1[0]) is not None
+    say("pipeline cache methods: second rollout")
+    second = _rollout(m, pipe.kv_cache1[0], P, T, L, N, KL, KG, n, H, D, seed=12)
+    for i, (x, y) in enumerate(zip(first, second)):
+        assert torch.equal(x, y), i

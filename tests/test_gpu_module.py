@@ -172,3 +172,85 @@ def test_forward_hier_membership_logits():
     err = (lg.grad.cpu() - lf.grad).abs()
     assert err.max() <= 2e-2 and err.mean() <= 2e-3
     assert _rel(lg.grad.cpu(), lf.grad) < 2e-2
+
+
+FLEX_CASES = [
+    # name, P, T, L, N, KL, KG, n, W, H, D, kind
+    ("labels_inactive", 4, 6, 20, 3, 5, 6, 3, 4, 2, 128, "labels"),
+    ("membership", 4, 6, 16, 2, 5, 6, 3, -1, 2, 64, "membership"),
+]
+
+
+@pytest.mark.parametrize("case", FLEX_CASES, ids=[c[0] for c in FLEX_CASES])
+def test_flex_block_mask_path(case):
+    """The production call path: ``build_stage2_hier_flex_block_mask`` as
+    WanModel.forward calls it (positional arguments, wan_video_dit.py:639-655),
+    then ``SelfAttention.forward(x, freqs, mask, cam_tokens=...)`` as
+    blocks.py:203 calls it.  Against the dense-mask SDPA of the same projected
+    Q/K/V (the mask the Flex BlockMask encodes, including an inactive hub
+    row's self edge) in fp32, for the output and, under autograd, for dL/dx
+    and the weight gradients; the no-grad (fused prologue) path too."""
+    need_gpu()
+    from multics_amd.hier_masks import HierBlockMask, build_stage2_hier_flex_block_mask
+    from oracle.masks import inactive_local_rows, mask_rows
+    name, P, T, L, N, KL, KG, n, W, H, D, kind = case
+    dim = H * D
+    m = _module(dim, H, seed=11)
+    m.num_frame_per_block, m.local_attn_size = n, W
+    rng = np.random.default_rng(12)
+    if kind == "labels":
+        labels = torch.tensor([[p % 2 for p in range(P)]] * T)        # slot 2 never used
+        topo = FullTopology(P, T, L, N, KL, KG, n, W, True, labels=labels.numpy())
+        mask, S, S_pad = build_stage2_hier_flex_block_mask(P, T, L, N, KL, KG, n, W, labels,
+                                                           None, True, "cuda")
+    else:
+        mem = np.repeat(rng.random((T // n, N, P)) < 0.5, n, axis=0)
+        go = ~mem.any(1)
+        topo = FullTopology(P, T, L, N, KL, KG, n, W, True, membership=mem, global_only=go)
+        mask, S, S_pad = build_stage2_hier_flex_block_mask(
+            P, T, L, N, KL, KG, n, W, None, None, True, "cuda",
+            membership=torch.from_numpy(mem), global_only=torch.from_numpy(go))
+    assert isinstance(mask, HierBlockMask) and S == topo.S and S_pad % 128 == 0
+    assert mask.shape[-1] == S_pad
+    dead = inactive_local_rows(topo)
+    assert len(mask.self_rows) == dead.sum() and (kind != "labels" or dead.any())
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(1, S, dim, generator=g).to("cuda", torch.bfloat16)
+    cam = torch.randn(1, S, 12, generator=g).to("cuda", torch.bfloat16)
+    dy = torch.randn(1, S, dim, generator=g).to("cuda", torch.bfloat16)
+    freqs = _freqs(S, D, 14)
+    say("flex block-mask path", name, S)
+    xg = x.clone().requires_grad_(True)
+    y = m(xg, freqs, mask, cam_tokens=cam)
+    y.backward(dy)
+    with torch.no_grad():
+        y_ng = m(x, freqs, mask, cam_tokens=cam)
+    torch.cuda.synchronize()
+    # fp32 reference: the module's math with dense-mask SDPA
+    mf = SelfAttention(dim, H, eps=1e-6)
+    mf.enable_camera_pose_qk(12, dropout_p=0.0)
+    mf.load_state_dict({k_: v_.float().cpu() for k_, v_ in m.state_dict().items()})
+    xf = x.float().cpu().requires_grad_(True)
+    q, k, v = mf._project_self_attn_qkv(xf, freqs, cam.float().cpu())
+    dm = torch.from_numpy(mask_rows(topo))
+    sp = lambda t: t.view(1, S, H, D).transpose(1, 2)
+    att = torch.nn.functional.scaled_dot_product_attention(sp(q), sp(k), sp(v), attn_mask=dm)
+    yf = mf.o(att.transpose(1, 2).reshape(1, S, dim))
+    yf.backward(dy.float().cpu())
+    mx, mn = err_stats(y.detach(), yf.detach())
+    mx2, mn2 = err_stats(y_ng, yf.detach())
+    say(f"  out max-abs {mx:.3e} mean-abs {mn:.3e}; no-grad {mx2:.3e} / {mn2:.3e}")
+    assert mx <= 2e-2 and mn <= 2e-3 and mx2 <= 2e-2 and mn2 <= 2e-3
+    for nm, got, want in (("dx", xg.grad.cpu(), xf.grad), ("dWv", m.v.weight.grad.cpu(),
+                                                          mf.v.weight.grad),
+                          ("dWq", m.q.weight.grad.cpu(), mf.q.weight.grad),
+                          ("dWcamk", m.cam_k.weight.grad.cpu(), mf.cam_k.weight.grad)):
+        say(f"  {nm} rel {_rel(got, want):.3e} rel-mean {_rel_mean(got, want):.3e}")
+        assert _rel(got, want) < 2e-2 and _rel_mean(got, want) < 1e-2, nm
+    # a second call with the same topology returns the cached mask
+    again = build_stage2_hier_flex_block_mask(P, T, L, N, KL, KG, n, W,
+                                              labels if kind == "labels" else None, None, True,
+                                              "cuda", **({} if kind == "labels" else dict(
+                                                  membership=torch.from_numpy(mem),
+                                                  global_only=torch.from_numpy(go))))
+    assert again[0] is mask
