@@ -19,8 +19,12 @@
 // into one FMA -- the numerics of the reference kernels
 // (hier_tiled_attention.py:112-143); the row sum l adds the bf16-rounded P
 // (v_dot2_f32_bf16), i.e. exactly the weights that multiply V.  The running max
-// is refreshed lazily: O and l are rescaled only when a row's max grows by more
-// than 2^8 in exp2 units.  Rows with no visible key output 0
+// is refreshed lazily: a block's P is computed against the running max of the
+// blocks before it, so the exps need no block max first; only when a lane's
+// block sum exceeds 16 * 2^8 (some score more than 2^8 above that max in exp2
+// units; always at a row's first visible key) does the wave take the block
+// max, recompute P and rescale O and l.  An accepted P is thus at most 2^12.
+// Rows with no visible key output 0
 // (hier_segmented_attention.py:104-109).
 //
 // Workgroup = 4 waves x 32 query rows (128 rows per work item), two
@@ -45,7 +49,14 @@ using namespace hier::tile;
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr float kRescaleLog2 = 8.0f;   // lazy-rescale threshold (exp2 units)
+// A lane's sum of its 16 P values of a block (each 2^(score - running max) in
+// exp2 units) above this bound refreshes the running max.
+constexpr float kSumMax = 16.f * 256.f;
+// Running max of a row that has seen no visible key: finite, so the exp2
+// offset -m * c2 stays finite, and a masked score (-inf) still gives P = 0.
+constexpr float kNoMax = -1e30f;
+constexpr int kValuPerMfma = 3;       // softmax VALU instructions scheduled after each MFMA
+constexpr bool kSplitSmall = true;     // items of <= 32 rows: two waves split the key blocks
 
 // LDS stages of a workgroup: K[2], V[2], masks[2] (one dword per key), each
 // its own __shared__ array.  K tiles are only read as rows, V tiles only
@@ -87,7 +98,7 @@ __device__ __forceinline__ void rows_init(Rows<D>& R, const HierFwdArgs& a, cons
   for (int db = 0; db < Geo<D>::NDB; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) R.o[db][i] = 0.f;
-  R.m = -INFINITY;
+  R.m = kNoMax;
   R.l = 0.f;
   R.alpha = 1.f;
 }
@@ -136,21 +147,10 @@ __device__ __forceinline__ void mask_block(f32x16& s, const char* mslot, int kb,
   }
 }
 
-// Online softmax of one 32-key block (branch-free).  Writes P (bf16) as the two
-// P^T operands of the block, updates m / l and R.alpha; returns whether any
-// lane of the wave needs its O rescaled by alpha before the next P.V.
-template <int D>
-__device__ __forceinline__ bool softmax_block(Rows<D>& R, const f32x16& s, bf16x8* p, float c2,
-                                              float thr) {
-  float mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[i], s[i + 1]));
-  mx = pair_max(mx);
-  const bool any = __ballot(mx > R.m + thr) != 0;
-  const float m_new = any ? fmaxf(R.m, mx) : R.m;
-  R.alpha = (m_new == R.m) ? 1.f : __builtin_amdgcn_exp2f((R.m - m_new) * c2);
-  R.m = m_new;
-  const float nb = (m_new == -INFINITY) ? 0.f : -m_new * c2;
+// P of one 32-key block: exp2(s * c2 + nb) rounded to bf16, written as the
+// two P^T operands of the block; returns the lane's sum of the rounded P
+// (v_dot2_f32_bf16 against ones), i.e. exactly the weights that multiply V.
+__device__ __forceinline__ float p_block(const f32x16& s, bf16x8* p, float c2, float nb) {
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     p[i >> 3][i & 7] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[i], c2, nb));
@@ -163,8 +163,37 @@ __device__ __forceinline__ bool softmax_block(Rows<D>& R, const f32x16& s, bf16x
     ps0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[c], p[c], 4, 5), one, ps0, false);
     ps1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[c], p[c], 6, 7), one, ps1, false);
   }
-  R.l = R.l * R.alpha + (ps0 + ps1);
-  return any;
+  return ps0 + ps1;
+}
+
+// Online softmax, second half: ps is the lane's sum of a block's P taken
+// against the running max R.m (p_block with nb = -R.m * c2).  While every
+// lane's sum stays <= kSumMax the block is accepted as it is.  Otherwise
+// (and always for a row's first visible key, while R.m = kNoMax) the wave
+// takes the block max, recomputes P against the new max and returns true: O
+// must be rescaled by R.alpha before the next P.V.
+template <int D>
+__device__ __forceinline__ bool softmax_fix(Rows<D>& R, const f32x16& s, bf16x8* p, float c2,
+                                            float ps) {
+  if (__ballot(!(ps <= kSumMax)) == 0) {
+    R.l += ps;
+    R.alpha = 1.f;
+    return false;
+  }
+  float mx = s[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+  mx = pair_max(mx);
+  const float m_new = fmaxf(R.m, mx);
+  R.alpha = __builtin_amdgcn_exp2f((R.m - m_new) * c2);
+  R.m = m_new;
+  R.l = R.l * R.alpha + p_block(s, p, c2, -m_new * c2);
+  return true;
+}
+
+template <int D>
+__device__ __forceinline__ bool softmax_block(Rows<D>& R, const f32x16& s, bf16x8* p, float c2) {
+  return softmax_fix<D>(R, s, p, c2, p_block(s, p, c2, -R.m * c2));
 }
 
 template <int D>
@@ -225,7 +254,7 @@ struct Ctx {
   const uint32_t* kv_mask;   // tile_kv_mask + kv_off
   const uint32_t* blk;       // tile_blk_and + kv_off / 64
   uint32_t k_ss_b, v_ss_b;
-  float c2, thr;
+  float c2;
   int nt, wave, lane;
   bool active;
   Copier<D, kRowRead> ck;
@@ -248,8 +277,7 @@ __device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
                                           const Stages& st) {
   if (resc) rescale<D>(R, alpha_pend);
   sq = qk_block<D>(R.q, st.k[PAR ^ 1], c.ra, B);
-  resc = softmax_block<D>(R, sc, pn, c.c2, c.thr);
-  alpha_pend = R.alpha;
+  float ps = p_block(sc, pn, c.c2, -R.m * c.c2);
   pv_block<D>(R, pv, st.v[PAR], c.ra, B);
   // NC + 2*NDB MFMAs and NC + 4*NDB LDS reads: three reads per two MFMAs
   constexpr int NM = Geo<D>::NC + 2 * Geo<D>::NDB;
@@ -261,11 +289,13 @@ __device__ __forceinline__ void half_step(Ctx<D>& c, Rows<D>& R, int t, f32x16& 
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     else
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
   }
   // keep the softmax results in this region (otherwise they sink past the
-  // mask branch, away from the MFMAs they are meant to overlap)
-  asm volatile("" : "+v"(pn[0]), "+v"(pn[1]), "+v"(R.l), "+v"(alpha_pend));
+  // branches below, away from the MFMAs they are meant to overlap)
+  asm volatile("" : "+v"(pn[0]), "+v"(pn[1]), "+v"(ps));
+  resc = softmax_fix<D>(R, sc, pn, c.c2, ps);
+  alpha_pend = R.alpha;
   if ((blk_cur & R.bits) != R.bits)
     mask_block(sq, st.m[PAR ^ 1], B, R.qframe, c.lane);
 }
@@ -308,12 +338,181 @@ __device__ __forceinline__ void tail(Ctx<D>& c, Rows<D>& R, const HierFwdArgs& a
                                      float alpha_pend, const Stages& st) {
   const char* vs = st.v[PAR];
   if (resc) rescale<D>(R, alpha_pend);
-  resc = softmax_block<D>(R, sb, pb, c.c2, c.thr);
+  resc = softmax_block<D>(R, sb, pb, c.c2);
   alpha_pend = R.alpha;
   pv_block<D>(R, pa, vs, c.ra, 0);
   if (resc) rescale<D>(R, alpha_pend);
   pv_block<D>(R, pb, vs, c.ra, 1);
   store_rows<D>(R, a, head, c.lane, pair_sum(R.l), R.m);
+}
+
+// ---- items of at most 32 rows ----------------------------------------------
+//
+// A hub slot's rows (15 or 18 at n = 3) and the 20-row tail of a 660-row player
+// block fill one 32-row sub-block, so in the loop above only wave 0 would
+// compute.  Such an item runs the same tile copies (all four waves, same
+// stages and barriers), but waves 0 and 1 both take its rows and each
+// computes one of the two 32-key blocks of every tile, with its own
+// online-softmax state; the two states are merged through LDS at the end.
+// Per iteration t a computing wave (block kb = wave) overlaps QK of tile t+1
+// with the softmax and P.V of tile t.
+
+template <int D, int PAR>
+__device__ __forceinline__ void split_iter(Ctx<D>& c, Rows<D>& R, int t, f32x16& s, Idx<D>& ik,
+                                           Idx<D>& iv, uint32_t& blk, const Stages& st) {
+  if (t + 2 < c.nt) {
+    copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, ik, st.k[PAR], c.wave);
+    if (c.wave == 0)
+      copy_dwords(c.kv_mask + (t + 2) * kSlab, st.m[PAR], c.lane);
+  }
+  ik = load_idx<D>(c.kv_idx, min(t + 3, c.nt - 1), c.ck.idx_off);
+  const uint32_t blk_pre = c.blk[min(t + 2, c.nt - 1)];
+  copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, iv, st.v[PAR ^ 1], c.wave);
+  iv = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+  if (c.active) {
+    const int kb = c.wave;
+    f32x16 sn = qk_block<D>(R.q, st.k[PAR ^ 1], c.ra, kb);
+    bf16x8 p[2];
+    if (softmax_block<D>(R, s, p, c.c2)) rescale<D>(R, R.alpha);
+    pv_block<D>(R, p, st.v[PAR], c.ra, kb);
+    if ((blk & R.bits) != R.bits) mask_block(sn, st.m[PAR ^ 1], kb, R.qframe, c.lane);
+    s = sn;
+  }
+  wait_copies();
+  __syncthreads();
+  blk = blk_pre;
+}
+
+// Last tile of a split item, then the merge of the two waves' states: row
+// maxima through LDS, then l and O rescaled to the common maximum (O^T as
+// fp32 [d-block][element][lane] in the wave's idle K stage), summed by one
+// wave per 32-wide d-block.
+template <int D, int PAR>
+__device__ __forceinline__ void split_tail(Ctx<D>& c, Rows<D>& R, const HierFwdArgs& a, int head,
+                                           f32x16& s, const Stages& st) {
+  if (c.active) {
+    bf16x8 p[2];
+    if (softmax_block<D>(R, s, p, c.c2)) rescale<D>(R, R.alpha);
+    pv_block<D>(R, p, st.v[PAR], c.ra, c.wave);
+  }
+  const int q = c.lane & 31;
+  float* m_lds = reinterpret_cast<float*>(st.m[0]);
+  float* l_lds = reinterpret_cast<float*>(st.m[1]);
+  const float l_w = pair_sum(R.l);
+  __syncthreads();                 // every wave is done with the stages
+  if (c.active && c.lane < 32) m_lds[c.wave * 32 + q] = R.m;
+  __syncthreads();
+  const float m_tot = fmaxf(m_lds[q], m_lds[32 + q]);
+  if (c.active) {
+    const float alpha = __builtin_amdgcn_exp2f((R.m - m_tot) * c.c2);
+    if (c.lane < 32) l_lds[c.wave * 32 + q] = l_w * alpha;
+    float* o_own = reinterpret_cast<float*>(c.wave == 0 ? st.k[0] : st.k[1]);
+#pragma unroll
+    for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o_own[(db * 16 + e) * 64 + c.lane] = R.o[db][e] * alpha;
+  }
+  __syncthreads();
+  if (c.wave >= Geo<D>::NDB) return;
+  const float l_tot = l_lds[q] + l_lds[32 + q];
+  const int db = c.wave;
+  if (!R.valid) return;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float* o0 = reinterpret_cast<const float*>(st.k[0]);
+  const float* o1 = reinterpret_cast<const float*>(st.k[1]);
+  uint16_t* op = a.o + (int64_t)R.qtok * a.o_ss + (int64_t)head * a.o_sh;
+  const int half = c.lane >> 5;
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    float v4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = (db * 16 + 4 * g4 + e) * 64 + c.lane;
+      v4[e] = (o0[k] + o1[k]) * inv;
+    }
+    u32x2 w;
+    w[0] = (uint32_t)f2bf(v4[0]) | ((uint32_t)f2bf(v4[1]) << 16);
+    w[1] = (uint32_t)f2bf(v4[2]) | ((uint32_t)f2bf(v4[3]) << 16);
+    *reinterpret_cast<u32x2*>(op + db * 32 + 8 * g4 + 4 * half) = w;
+  }
+  if (a.lse && db == 0 && half == 0)
+    a.lse[(int64_t)head * a.lse_stride_h + R.qtok] =
+        l_tot > 0.f ? m_tot * a.scale + __logf(l_tot) : -INFINITY;
+}
+
+// Common set-up of both item kinds: the lane's copy and read offsets, the
+// item's key list, the first tiles resident in LDS.
+template <int D>
+__device__ __forceinline__ void item_setup(Ctx<D>& c, const HierFwdArgs& a, const int32_t* it,
+                                           int head, int tid, bool active) {
+  c.lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kv_off = it[5], kv_cnt = it[6];
+  c.nt = kv_cnt / kSlab;
+  c.active = active;
+  c.c2 = a.scale * 1.4426950408889634f;
+  c.gk = reinterpret_cast<const char*>(a.k + (int64_t)head * a.k_sh);
+  c.gv = reinterpret_cast<const char*>(a.v + (int64_t)head * a.v_sh);
+  c.k_ss_b = (uint32_t)(a.k_ss * 2);
+  c.v_ss_b = (uint32_t)(a.v_ss * 2);
+  c.kv_idx = a.tile_kv_idx + kv_off;
+  c.kv_mask = a.tile_kv_mask + kv_off;
+  c.blk = a.tile_blk_and + kv_off / kSlab;
+  c.ck.init(c.wave, c.lane);
+  c.cv.init(c.wave, c.lane);
+  c.ra.init(c.lane);
+}
+
+// Prologue copies (nt >= 1): K(0), V(0), K(1) and masks(0, 1) resident; the
+// first iteration's indices and flags loaded before the wait.
+template <int D>
+__device__ __forceinline__ void prologue_copies(Ctx<D>& c, Idx<D>& ik, Idx<D>& iv, uint32_t& blk,
+                                                const Stages& st) {
+  const int nt = c.nt;
+  const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
+  copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i0, st.k[0], c.wave);
+  copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, i0, st.v[0], c.wave);
+  if (c.wave == 0) copy_dwords(c.kv_mask, st.m[0], c.lane);
+  if (nt > 1) {
+    const Idx<D> i1 = load_idx<D>(c.kv_idx, 1, c.ck.idx_off);
+    copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i1, st.k[1], c.wave);
+    if (c.wave == 0) copy_dwords(c.kv_mask + kSlab, st.m[1], c.lane);
+  }
+  ik = load_idx<D>(c.kv_idx, min(2, nt - 1), c.ck.idx_off);
+  iv = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
+  blk = c.blk[min(1, nt - 1)];
+  wait_copies();
+  __syncthreads();
+}
+
+template <int D>
+__device__ __forceinline__ void split_item(const HierFwdArgs& a, const int32_t* it, int head, int tid,
+                                        const Stages& st) {
+  Ctx<D> c;
+  item_setup<D>(c, a, it, head, tid, (tid >> 6) < 2);
+  Rows<D> R;
+  rows_init<D>(R, a, it, head, 0, c.lane);
+  const int nt = c.nt;
+  Idx<D> ik, iv;
+  uint32_t blk;
+  prologue_copies<D>(c, ik, iv, blk, st);
+  f32x16 s;
+  if (c.active) {
+    s = qk_block<D>(R.q, st.k[0], c.ra, c.wave);
+    if ((c.blk[0] & R.bits) != R.bits) mask_block(s, st.m[0], c.wave, R.qframe, c.lane);
+  }
+  __syncthreads();   // every wave has read K stage 0 and masks stage 0
+  int t = 0;
+  for (; t + 2 < nt; t += 2) {
+    split_iter<D, 0>(c, R, t, s, ik, iv, blk, st);
+    split_iter<D, 1>(c, R, t + 1, s, ik, iv, blk, st);
+  }
+  if (t + 1 < nt) {
+    split_iter<D, 0>(c, R, t, s, ik, iv, blk, st);
+    split_tail<D, 1>(c, R, a, head, s, st);
+  } else {
+    split_tail<D, 0>(c, R, a, head, s, st);
+  }
 }
 
 template <int D>
@@ -330,27 +529,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
   const int head = logical / a.n_items;
   const int item = logical - head * a.n_items;
   const int32_t* it = a.tile_items + (int64_t)item * 8;
-
   const int tid = threadIdx.x;
-  Ctx<D> c;
-  c.lane = tid & 63;
-  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row_count = it[4], kv_off = it[5], kv_cnt = it[6];
-  c.nt = kv_cnt / kSlab;
-  c.active = c.wave * 32 < row_count;
-  c.c2 = a.scale * 1.4426950408889634f;
-  c.thr = kRescaleLog2 / c.c2;
-  c.gk = reinterpret_cast<const char*>(a.k + (int64_t)head * a.k_sh);
-  c.gv = reinterpret_cast<const char*>(a.v + (int64_t)head * a.v_sh);
-  c.k_ss_b = (uint32_t)(a.k_ss * 2);
-  c.v_ss_b = (uint32_t)(a.v_ss * 2);
-  c.kv_idx = a.tile_kv_idx + kv_off;
-  c.kv_mask = a.tile_kv_mask + kv_off;
-  c.blk = a.tile_blk_and + kv_off / kSlab;
-  c.ck.init(c.wave, c.lane);
-  c.cv.init(c.wave, c.lane);
-  c.ra.init(c.lane);
+  const int row_count = it[4];
+  if (row_count <= 32 && it[6] >= 2 * kSlab && kSplitSmall) {
+    split_item<D>(a, it, head, tid, st);
+    return;
+  }
 
+  Ctx<D> c;
+  item_setup<D>(c, a, it, head, tid, (tid >> 6) * 32 < row_count);
   Rows<D> R;
   rows_init<D>(R, a, it, head, c.wave * 32, c.lane);
   const int nt = c.nt;
@@ -359,30 +546,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
     return;
   }
   char* const kst0 = st.k[0];
-  char* const vst0 = st.v[0];
   char* const mst0 = st.m[0];
 
-  // prologue: K(0), V(0), K(1) and masks(0, 1) resident; S(0), S(1) (both
-  // blocks of tile 0) computed and masked; P(0) from the softmax of S(0); the
-  // first iteration's indices and flags loaded before the wait.
+  // prologue: the first tiles resident; S(0), S(1) (both blocks of tile 0)
+  // computed and masked; P(0) from the softmax of S(0)
   Idx<D> ik, iv;
   uint32_t blk;
-  {
-    const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
-    copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i0, kst0, c.wave);
-    copy_tile<D, kTrRead>(c.gv, c.v_ss_b, c.cv, i0, vst0, c.wave);
-    if (c.wave == 0) copy_dwords(c.kv_mask, mst0, c.lane);
-    if (nt > 1) {
-      const Idx<D> i1 = load_idx<D>(c.kv_idx, 1, c.ck.idx_off);
-      copy_tile<D, kRowRead>(c.gk, c.k_ss_b, c.ck, i1, st.k[1], c.wave);
-      if (c.wave == 0) copy_dwords(c.kv_mask + kSlab, st.m[1], c.lane);
-    }
-    ik = load_idx<D>(c.kv_idx, min(2, nt - 1), c.ck.idx_off);
-    iv = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
-    blk = c.blk[min(1, nt - 1)];
-    wait_copies();
-    __syncthreads();
-  }
+  prologue_copies<D>(c, ik, iv, blk, st);
   f32x16 sa, sb;
   bf16x8 pa[2], pb[2];
   bool resc = false;
@@ -394,7 +564,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(HierFwdArgs a, in
       mask_block(sa, mst0, 0, R.qframe, c.lane);
       mask_block(sb, mst0, 1, R.qframe, c.lane);
     }
-    resc = softmax_block<D>(R, sa, pa, c.c2, c.thr);
+    resc = softmax_block<D>(R, sa, pa, c.c2);
     alpha_pend = R.alpha;
   }
   __syncthreads();   // every wave has read K stage 0 and masks stage 0
