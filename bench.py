@@ -265,18 +265,42 @@ def bench_training(dev, steps=10, warmup=3):
         q.grad = k.grad = v.grad = lg.grad = None
         fwd().backward(dout)
 
+    def rebuild():
+        """The lists of the current logits, built from scratch (no cache):
+        membership read back, both device metadata passes, both device
+        backward-list passes."""
+        from multics_amd import metadata as M
+        m = (lg.detach() > 0).cpu().numpy()
+        t_ = M.build(M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                              direct=True, membership=m, global_only=~m.any(1)),
+                     dev).tiles
+        M.backward_lists(t_, geo)
+        return t_
+
+    def step_rebuild():
+        t_ = rebuild()
+        q.grad = k.grad = v.grad = lg.grad = None
+        hier_attention(q, k, v, t_, membership_logits=lg, ste_geometry=geo).backward(dout)
+
     ms_fwd = float(np.median(time_events(lambda: fwd(), steps, warmup)))
     ms_step = float(np.median(time_events(step, steps, warmup)))
+    ms_meta = float(np.median(time_events(rebuild, steps, warmup)))
+    ms_step_rebuild = float(np.median(time_events(step_rebuild, steps, warmup)))
     E = tiles.logical_pairs
     flop_f, flop_b = 4.0 * H * D * E, 10.0 * H * D * E
     ms_bwd = ms_step - ms_fwd
     return {"players": P, "frames": T, "window": W, "tokens": S, "useful_pairs": E,
             "ms_fwd": round(ms_fwd, 4), "ms_fwd_bwd": round(ms_step, 4),
             "ms_bwd": round(ms_bwd, 4),
+            "ms_metadata_rebuild": round(ms_meta, 4),
+            "ms_fwd_bwd_with_rebuild": round(ms_step_rebuild, 4),
             "useful_tflops_fwd_bwd": round((flop_f + flop_b) / (ms_step * 1e-3) / 1e12, 2),
             "useful_tflops_bwd": round(flop_b / (ms_bwd * 1e-3) / 1e12, 2),
             "note": "bwd = dQ (query-major) + dK/dV (key-major) + membership STE pass; "
-                    "useful FLOP 4*H*D*E fwd, 10*H*D*E bwd"}
+                    "useful FLOP 4*H*D*E fwd, 10*H*D*E bwd; *_rebuild: every step rebuilds "
+                    "the forward, key-major and STE lists from the logits on the device "
+                    "(membership read back, two count read-backs), as a step whose logits "
+                    "flipped membership must"}
 
 
 def bench_rollout(dev, passes=10):

@@ -131,6 +131,52 @@ int hier_meta_count(const HierTopo* topo, const HierMetaCounts* counts, void* st
 int hier_meta_build(const HierTopo* topo, const HierMetaOut* out, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Backward lists derived on the device from a full-sequence tile list:     */
+/* the key-major list of the dK / dV passes and the membership-STE list,    */
+/* bit for bit the host builders transpose_tiles / ste_tiles of             */
+/* multics_amd/metadata.py.  No reference counterpart: the reference's      */
+/* backward is FlexAttention's autograd over its BlockMask                  */
+/* (multics/models/attention.py:322-353, 367-434).                          */
+/* ------------------------------------------------------------------------ */
+typedef struct HierDeriveArgs {
+  /* forward tile list (DEVICE) */
+  int32_t n_items;          /* work items                                       */
+  int32_t n_groups;         /* (block, stream) groups = items with row_start 0   */
+  int32_t rows;             /* 1 + largest row / key index (queries = keys)      */
+  int32_t nq_max;           /* largest frame count of a group (<= 32)            */
+  int32_t kv_len;           /* entries of kv_idx / kv_mask                       */
+  int32_t P, T, L, N, KL;   /* STE geometry (token order of the full sequence)   */
+  const int32_t* items;     /* [n_items][8]                                      */
+  const int32_t* kv_idx;
+  const uint32_t* kv_mask;
+  /* workspace (DEVICE, hier_derive_workspace bytes) and pass-1 results       */
+  void* ws;
+  int64_t ws_bytes;
+  int64_t* totals;          /* DEVICE [8]: key-major entries, pairs, STE entries, */
+                            /* STE items, error bits (1 token in two groups,      */
+                            /* 2 key outside every group, 4 not whole key frames, */
+                            /* 8 malformed items, 16 offset overflow)             */
+  /* pass 2: sizes read back from totals, output arrays (DEVICE)              */
+  int64_t key_entries, ste_entries;
+  int32_t* key_items;       /* [n_items][8]                                      */
+  int32_t* key_q_idx;       /* [key_entries]                                     */
+  uint32_t* key_q_mask;
+  uint32_t* key_blk_and;    /* [key_entries / 64]                                */
+  int32_t* ste_items;       /* [totals[3]][8]                                    */
+  int32_t* ste_kv_idx;      /* [ste_entries]                                     */
+  uint32_t* ste_kv_mask;
+  uint32_t* ste_blk_and;    /* [ste_entries / 64]                                */
+  int32_t* ste_kv_class;    /* [ste_entries]                                     */
+} HierDeriveArgs;
+
+/* Workspace bytes for the sizes in args (ws may be NULL); -1 on NULL args.  */
+int64_t hier_derive_workspace(const HierDeriveArgs* args);
+/* Pass 1: groups, token map, run table, list sizes and offsets -> totals.   */
+int hier_derive_count(const HierDeriveArgs* args, void* stream);
+/* Pass 2: the two lists, their per-64 mask ANDs and their items.            */
+int hier_derive_build(const HierDeriveArgs* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Q/K/V layout prologue: camera-pose Q/K adapter, RMSNorm over all heads,  */
 /* gain and RoPE fused into one pass that writes the attention layout.       */
 /* Replaces SelfAttention._project_self_attn_qkv after the three GEMMs      */

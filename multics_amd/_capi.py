@@ -105,9 +105,22 @@ class HierFrameAttnArgs(C.Structure):
                [("q_frame", vp), ("k_frame", vp)]
 
 
+class HierDeriveArgs(C.Structure):
+    _fields_ = [(n, i32) for n in ("n_items", "n_groups", "rows", "nq_max", "kv_len", "P", "T",
+                                   "L", "N", "KL")] + \
+               [(n, vp) for n in ("items", "kv_idx", "kv_mask", "ws")] + \
+               [("ws_bytes", i64), ("totals", vp), ("key_entries", i64), ("ste_entries", i64)] + \
+               [(n, vp) for n in ("key_items", "key_q_idx", "key_q_mask", "key_blk_and",
+                                  "ste_items", "ste_kv_idx", "ste_kv_mask", "ste_blk_and",
+                                  "ste_kv_class")]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
+    "hier_derive_workspace": [C.POINTER(HierDeriveArgs)],
+    "hier_derive_count": [C.POINTER(HierDeriveArgs), vp],
+    "hier_derive_build": [C.POINTER(HierDeriveArgs), vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],
@@ -135,7 +148,8 @@ def lib() -> C.CDLL:
             for name, argtypes in EXPORTS.items():
                 fn = getattr(handle, name)
                 fn.argtypes = argtypes
-                fn.restype = C.c_char_p if name in ("hier_last_error", "hier_version") else C.c_int
+                fn.restype = C.c_char_p if name in ("hier_last_error", "hier_version") else \
+                    (C.c_int64 if name == "hier_derive_workspace" else C.c_int)
             _lib = handle
     return _lib
 

@@ -20,6 +20,8 @@
 // Integer work only; HBM-bound and tiny (a few MB per topology).
 #include "hier_common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -610,4 +612,569 @@ extern "C" int hier_meta_build(const HierTopo* topo, const HierMetaOut* out, voi
   hipLaunchKernelGGL(meta_build_kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream,
                      *topo, *out);
   return hier::check_launch("meta_build_kernel");
+}
+
+// ---- backward lists derived from a full-sequence tile list -----------------
+//
+// The dK / dV passes of the backward walk a key-major list and the membership
+// STE pass a list of the membership-gated edges; both follow from the forward
+// tile list alone.  In a full-sequence topology every token is a query row of
+// exactly one (block, stream) group (the items that share one key list) and a
+// key of the same group, and a group's key list is a concatenation of whole
+// key frames ("runs") of groups, each run with one bitmask over the query
+// group's frames.
+//
+//   key-major list of key group G: the query units (g, j) -- query group g,
+//     its frame j -- that see any frame of G, in (g, j) order, each unit's
+//     qlen(g) rows with the bitmask over G's frames it sees; padded to 64
+//     with (row 0, mask 0).  Items: the forward items with the key offset /
+//     count of their group's list.
+//   STE list of group g: player groups keep their local-hub keys (class =
+//     group), local-hub groups their player keys (class = player), in list
+//     order stably grouped by class, padded to 64; global-hub groups and
+//     groups without such a key are dropped.
+//
+// Pass 1 (hier_derive_count) maps tokens to groups, collects the runs into a
+// dense [key group][query group][query frame] table of key-frame bitmasks,
+// counts both lists and prefix-sums their offsets; the caller reads back the
+// totals (entries, pairs, error flags) to size pass 2 (hier_derive_build),
+// which writes the lists, the per-64-key ANDs of the masks and the items.
+
+namespace {
+
+constexpr int kDeriveThreads = 256;
+constexpr int kScanThreads = 1024;
+constexpr int kClasses = 64;            // STE classes (players or groups, <= 62)
+constexpr int64_t kMaxTable = 1ll << 26;  // n_groups^2 * nq_max table entries
+
+enum DeriveErr {
+  kErrTwoGroups = 1,      // a token is a query row of two groups
+  kErrNoGroup = 2,        // a key is not a query row of any group
+  kErrRuns = 4,           // key lists are not whole key frames
+  kErrItems = 8,          // items are not grouped / frames exceed nq_max
+  kErrOverflow = 16       // a list offset does not fit in int32
+};
+
+struct DeriveWs {
+  int32_t* grp_of_item;   // [n_items]
+  int32_t* grp_first;     // [n_groups + 1]
+  int32_t* tok_g;         // [rows]
+  int32_t* tok_r;         // [rows]
+  uint32_t* table;        // [n_groups][n_groups][nq]: (key group G, query group g, frame j)
+  int32_t* runs;          // [n_groups][n_groups][nq]: runs of (query g, key group G, key frame f)
+  int32_t* t_size;        // [n_groups] padded key-major list sizes
+  int64_t* t_off;         // [n_groups + 1]
+  int32_t* s_cnt;         // [n_groups][kClasses]
+  int32_t* s_size;        // [n_groups] padded STE list sizes
+  int64_t* s_off;         // [n_groups + 1]
+  int64_t* s_item_off;    // [n_groups + 1]
+};
+
+__host__ __device__ inline int64_t al256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+__host__ __device__ inline int64_t derive_ws_layout(const HierDeriveArgs& a, DeriveWs* w) {
+  const int64_t ng = a.n_groups, tab = ng * ng * a.nq_max;
+  int64_t o = 0;
+  char* base = reinterpret_cast<char*>(a.ws);
+  auto take = [&](int64_t bytes) { char* p = base ? base + o : nullptr; o += al256(bytes); return p; };
+  DeriveWs d;
+  d.grp_of_item = reinterpret_cast<int32_t*>(take(4 * (int64_t)a.n_items));
+  d.grp_first = reinterpret_cast<int32_t*>(take(4 * (ng + 1)));
+  d.tok_g = reinterpret_cast<int32_t*>(take(4 * (int64_t)a.rows));
+  d.tok_r = reinterpret_cast<int32_t*>(take(4 * (int64_t)a.rows));
+  d.table = reinterpret_cast<uint32_t*>(take(4 * tab));
+  d.runs = reinterpret_cast<int32_t*>(take(4 * tab));
+  d.t_size = reinterpret_cast<int32_t*>(take(4 * ng));
+  d.t_off = reinterpret_cast<int64_t*>(take(8 * (ng + 1)));
+  d.s_cnt = reinterpret_cast<int32_t*>(take(4 * ng * kClasses));
+  d.s_size = reinterpret_cast<int32_t*>(take(4 * ng));
+  d.s_off = reinterpret_cast<int64_t*>(take(8 * (ng + 1)));
+  d.s_item_off = reinterpret_cast<int64_t*>(take(8 * (ng + 1)));
+  if (w) *w = d;
+  return o;
+}
+
+__device__ __forceinline__ void flag(int64_t* totals, int e) {
+  atomicOr(reinterpret_cast<unsigned long long*>(&totals[4]), (unsigned long long)e);
+}
+
+__global__ void derive_fill_kernel(int32_t* p, int64_t n, int32_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// Block-wide exclusive scan of one value per thread (kScanThreads threads).
+__device__ int64_t block_scan(int64_t v, int64_t* sh, int64_t* total) {
+  const int t = threadIdx.x;
+  sh[t] = v;
+  __syncthreads();
+  for (int d = 1; d < kScanThreads; d <<= 1) {
+    const int64_t x = t >= d ? sh[t - d] : 0;
+    __syncthreads();
+    sh[t] += x;
+    __syncthreads();
+  }
+  const int64_t incl = sh[t];
+  *total = sh[kScanThreads - 1];
+  __syncthreads();
+  return incl - v;
+}
+
+// Groups: item i starts a group when its row_start is 0; grp_first[n_groups]
+// = n_items.  Totals zeroed.
+__global__ __launch_bounds__(kScanThreads) void derive_groups_kernel(HierDeriveArgs a, DeriveWs w) {
+  __shared__ int64_t sh[kScanThreads];
+  const int t = threadIdx.x;
+  if (t < 8) a.totals[t] = 0;
+  __syncthreads();
+  if (t == 0 && (a.n_items < 1 || a.items[3] != 0)) flag(a.totals, kErrItems);
+  int64_t carry = 0;
+  for (int base = 0; base < a.n_items; base += kScanThreads) {
+    const int i = base + t;
+    const int32_t* it = a.items + 8 * (int64_t)i;
+    const int start = (i < a.n_items && it[3] == 0) ? 1 : 0;
+    if (i < a.n_items && (it[7] < 1 || it[7] > a.nq_max || it[2] < 1 || it[5] < 0 ||
+                          it[6] < 0 || (int64_t)it[5] + it[6] > a.kv_len))
+      flag(a.totals, kErrItems);
+    int64_t tot;
+    const int64_t ex = block_scan(start, sh, &tot);
+    if (i < a.n_items) {
+      const int64_t g = carry + ex + start - 1;
+      w.grp_of_item[i] = (int32_t)min<int64_t>(max<int64_t>(g, 0), a.n_groups - 1);
+      if (start && g < a.n_groups) w.grp_first[g] = i;
+    }
+    carry += tot;
+  }
+  if (t == 0) {
+    if (carry != a.n_groups) flag(a.totals, kErrItems);
+    w.grp_first[a.n_groups] = a.n_items;
+  }
+}
+
+struct GroupDesc {
+  int qbase, qstride, qlen, off, cnt, n;
+};
+
+// A group's descriptor, from its first item; the key range is clamped to the
+// list (an item outside it is flagged by derive_groups_kernel).
+__device__ __forceinline__ GroupDesc group_desc(const HierDeriveArgs& a, const DeriveWs& w, int g) {
+  const int32_t* it = a.items + 8 * (int64_t)w.grp_first[g];
+  const int off = min(max(it[5], 0), a.kv_len);
+  const int cnt = min(max(it[6], 0), a.kv_len - off);
+  return {it[0], it[1], max(it[2], 1), off, cnt, it[7]};
+}
+
+// token -> (group, row inside the group); items of a group share its list.
+__global__ __launch_bounds__(kDeriveThreads) void derive_tokens_kernel(HierDeriveArgs a, DeriveWs w) {
+  const int g = blockIdx.x;
+  const GroupDesc d = group_desc(a, w, g);
+  for (int i = w.grp_first[g] + threadIdx.x; i < w.grp_first[g + 1]; i += blockDim.x) {
+    const int32_t* it = a.items + 8 * (int64_t)i;
+    if (it[0] != d.qbase || it[1] != d.qstride || it[2] != d.qlen || it[5] != d.off ||
+        it[6] != d.cnt || it[7] != d.n)
+      flag(a.totals, kErrItems);
+  }
+  const int nrows = d.n * d.qlen;
+  for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+    const int j = r / d.qlen;
+    const int64_t tok = (int64_t)d.qbase + (int64_t)j * d.qstride + (r - j * d.qlen);
+    if (tok < 0 || tok >= a.rows) {
+      flag(a.totals, kErrNoGroup);
+      continue;
+    }
+    if (atomicExch(&w.tok_g[tok], g) != -1) flag(a.totals, kErrTwoGroups);
+    w.tok_r[tok] = r;
+  }
+}
+
+// Runs of query group g's list: every live entry checks that the run of its
+// key frame starts where its row says, with the same mask, and is counted
+// against its (query group, key group, key frame); each run start checks the
+// run's last entry and sets its frame's bit in the key-major table for every
+// query frame of its mask.  A complete list has exactly qlen(key group) live
+// entries per (g, G, f) that occurs (checked by derive_key_sizes_kernel).
+__global__ __launch_bounds__(kDeriveThreads) void derive_runs_kernel(HierDeriveArgs a, DeriveWs w) {
+  const int g = blockIdx.x;
+  const GroupDesc d = group_desc(a, w, g);
+  const int ng = a.n_groups, nq = a.nq_max;
+  const int lane = threadIdx.x & 63;
+  const int32_t* idx = a.kv_idx + d.off;
+  const uint32_t* msk = a.kv_mask + d.off;
+  for (int i0 = 0; i0 < d.cnt; i0 += kDeriveThreads) {
+    const int i = i0 + threadIdx.x;
+    int64_t e = -1;                      // counted (g, G, f) of this entry
+    const uint32_t m = i < d.cnt ? msk[i] : 0u;
+    if (m != 0) {
+      const int k = idx[i];
+      const int G = (k >= 0 && k < a.rows) ? w.tok_g[k] : -1;
+      if (G < 0) {
+        flag(a.totals, kErrNoGroup);
+      } else {
+        const GroupDesc kg = group_desc(a, w, G);
+        const int r = w.tok_r[k], f = r / kg.qlen, rin = r - f * kg.qlen;
+        const int s = i - rin;
+        const int first_tok = kg.qbase + f * kg.qstride;
+        if (f < 0 || f >= nq || rin < 0 || s < 0 || idx[s] != first_tok || msk[s] != m) {
+          flag(a.totals, kErrRuns);
+        } else {
+          e = ((int64_t)g * ng + G) * nq + f;
+          if (rin == 0) {
+            const int last = i + kg.qlen - 1;
+            if (last >= d.cnt || idx[last] != first_tok + kg.qlen - 1 || msk[last] != m) {
+              flag(a.totals, kErrRuns);
+            } else {
+              for (int j = 0; j < nq; ++j)
+                if ((m >> j) & 1u) atomicOr(&w.table[((int64_t)G * ng + g) * nq + j], 1u << f);
+            }
+          }
+        }
+      }
+    }
+    // one atomic add per distinct run of the wave
+    uint64_t rem = __ballot(e >= 0);
+    while (rem) {
+      const int leader = __ffsll((unsigned long long)rem) - 1;
+      const int64_t el = __shfl(e, leader);
+      const uint64_t same = __ballot(e == el);
+      if (lane == leader) atomicAdd(&w.runs[el], (int)__popcll(same));
+      rem &= ~same;
+    }
+  }
+}
+
+// Key-major list size of key group G (padded to 64) and its (query, key) pairs.
+__global__ __launch_bounds__(kDeriveThreads) void derive_key_sizes_kernel(HierDeriveArgs a,
+                                                                          DeriveWs w) {
+  __shared__ int64_t s_size, s_pairs;
+  const int G = blockIdx.x;
+  const int ng = a.n_groups, nq = a.nq_max;
+  if (threadIdx.x == 0) s_size = s_pairs = 0;
+  __syncthreads();
+  const int qlen_G = group_desc(a, w, G).qlen;
+  int64_t size = 0, pairs = 0;
+  for (int u = threadIdx.x; u < ng * nq; u += blockDim.x) {
+    const int g = u / nq;
+    // runs is [query group][key group][key frame]: here query group G, key group g
+    const int n_live = w.runs[(int64_t)G * ng * nq + u];
+    if (n_live != 0 && n_live != group_desc(a, w, g).qlen) flag(a.totals, kErrRuns);
+    const uint32_t bits = w.table[(int64_t)G * ng * nq + u];
+    if (bits == 0) continue;
+    const int ql = group_desc(a, w, g).qlen;
+    size += ql;
+    pairs += (int64_t)ql * qlen_G * __popc(bits);
+  }
+  atomicAdd(reinterpret_cast<unsigned long long*>(&s_size), (unsigned long long)size);
+  atomicAdd(reinterpret_cast<unsigned long long*>(&s_pairs), (unsigned long long)pairs);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    w.t_size[G] = (int32_t)((s_size + kTileKeys - 1) / kTileKeys * kTileKeys);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&a.totals[1]), (unsigned long long)s_pairs);
+  }
+}
+
+// STE selection of one entry of group d's list: class, or -1 if not kept.
+__device__ __forceinline__ int ste_class(const HierDeriveArgs& a, const GroupDesc& d, int k,
+                                         uint32_t m) {
+  const int64_t a0 = (int64_t)a.P * a.T * a.L, g0 = a0 + (int64_t)a.T * a.N * a.KL;
+  if (m == 0) return -1;
+  if (d.qbase < a0) {
+    if (k < a0 || k >= g0) return -1;
+    return (int)(((k - a0) / max(a.KL, 1)) % max(a.N, 1));
+  }
+  if (k >= a0) return -1;
+  return (int)(k / ((int64_t)a.T * a.L));
+}
+
+__device__ __forceinline__ bool ste_group(const HierDeriveArgs& a, const GroupDesc& d) {
+  const int64_t a0 = (int64_t)a.P * a.T * a.L, g0 = a0 + (int64_t)a.T * a.N * a.KL;
+  return d.qbase < g0 && d.cnt > 0;
+}
+
+// Per-class counts of group g's STE list.
+__global__ __launch_bounds__(kDeriveThreads) void derive_ste_count_kernel(HierDeriveArgs a,
+                                                                         DeriveWs w) {
+  __shared__ int cnt[kClasses];
+  const int g = blockIdx.x;
+  for (int c = threadIdx.x; c < kClasses; c += blockDim.x) cnt[c] = 0;
+  __syncthreads();
+  const GroupDesc d = group_desc(a, w, g);
+  if (ste_group(a, d))
+    for (int i = threadIdx.x; i < d.cnt; i += blockDim.x) {
+      const int c = ste_class(a, d, a.kv_idx[d.off + i], a.kv_mask[d.off + i]);
+      if (c >= kClasses) flag(a.totals, kErrItems);
+      else if (c >= 0) atomicAdd(&cnt[c], 1);
+    }
+  __syncthreads();
+  int n = 0;
+  for (int c = 0; c < kClasses; ++c) n += cnt[c];
+  for (int c = threadIdx.x; c < kClasses; c += blockDim.x) w.s_cnt[g * kClasses + c] = cnt[c];
+  if (threadIdx.x == 0) w.s_size[g] = (n + kTileKeys - 1) / kTileKeys * kTileKeys;
+}
+
+// Offsets of both lists and of the STE items; totals [0] key-major entries,
+// [2] STE entries, [3] STE items.
+__global__ __launch_bounds__(kScanThreads) void derive_scan_kernel(HierDeriveArgs a, DeriveWs w) {
+  __shared__ int64_t sh[kScanThreads];
+  int64_t ct = 0, cs = 0, ci = 0;
+  for (int base = 0; base < a.n_groups; base += kScanThreads) {
+    const int g = base + threadIdx.x;
+    const bool in = g < a.n_groups;
+    const int64_t vt = in ? w.t_size[g] : 0, vs = in ? w.s_size[g] : 0;
+    const int64_t vi = (in && vs > 0) ? (int64_t)(w.grp_first[g + 1] - w.grp_first[g]) : 0;
+    int64_t tt, ts, ti;
+    const int64_t et = block_scan(vt, sh, &tt);
+    const int64_t es = block_scan(vs, sh, &ts);
+    const int64_t ei = block_scan(vi, sh, &ti);
+    if (in) {
+      w.t_off[g] = ct + et;
+      w.s_off[g] = cs + es;
+      w.s_item_off[g] = ci + ei;
+    }
+    ct += tt;
+    cs += ts;
+    ci += ti;
+  }
+  if (threadIdx.x == 0) {
+    w.t_off[a.n_groups] = ct;
+    w.s_off[a.n_groups] = cs;
+    w.s_item_off[a.n_groups] = ci;
+    a.totals[0] = ct;
+    a.totals[2] = cs;
+    a.totals[3] = ci;
+    if (ct > INT32_MAX || cs > INT32_MAX) flag(a.totals, kErrOverflow);
+  }
+}
+
+// Key-major list of key group G: unit offsets by a block scan over the
+// (g, j) units, then every entry finds its unit by binary search.
+__global__ __launch_bounds__(kScanThreads) void derive_key_write_kernel(HierDeriveArgs a,
+                                                                        DeriveWs w) {
+  __shared__ int64_t sh[kScanThreads];
+  __shared__ int32_t u_off[kScanThreads];
+  __shared__ int32_t u_id[kScanThreads];
+  const int G = blockIdx.x;
+  const int ng = a.n_groups, nq = a.nq_max, nu = ng * nq;
+  const int64_t base = w.t_off[G];
+  const int padded = w.t_size[G];
+  const uint32_t* row = w.table + (int64_t)G * nu;
+  int64_t done = 0;   // entries written before this chunk of units
+  for (int u0 = 0; u0 < nu; u0 += kScanThreads) {
+    const int u = u0 + threadIdx.x;
+    const int g = u / nq;
+    const bool live = u < nu && row[u] != 0;
+    const int len = live ? group_desc(a, w, g).qlen : 0;
+    int64_t chunk, n_live;
+    const int64_t ex = block_scan(len, sh, &chunk);
+    // the live units of this chunk, compacted in order
+    const int64_t li = block_scan(live ? 1 : 0, sh, &n_live);
+    if (live) {
+      u_off[li] = (int32_t)ex;
+      u_id[li] = u;
+    }
+    __syncthreads();
+    const int nl = (int)n_live;
+    for (int p = threadIdx.x; p < chunk; p += blockDim.x) {
+      int lo = 0, hi = nl - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (u_off[mid] <= p) lo = mid; else hi = mid - 1;
+      }
+      const int uu = u_id[lo], gg = uu / nq, j = uu - gg * nq;
+      const GroupDesc q = group_desc(a, w, gg);
+      const int r = p - u_off[lo];
+      a.key_q_idx[base + done + p] = q.qbase + j * q.qstride + r;
+      a.key_q_mask[base + done + p] = row[uu];
+    }
+    done += chunk;
+    __syncthreads();
+  }
+  for (int64_t p = done + threadIdx.x; p < padded; p += blockDim.x) {
+    a.key_q_idx[base + p] = 0;
+    a.key_q_mask[base + p] = 0;
+  }
+}
+
+// STE list of group g: entries in list order, stably grouped by class.  Each
+// chunk of 256 entries ranks its entries per class with wave ballots; a
+// running count per class carries the order across chunks.
+__global__ __launch_bounds__(kDeriveThreads) void derive_ste_write_kernel(HierDeriveArgs a,
+                                                                         DeriveWs w) {
+  __shared__ int cbase[kClasses];     // first position of each class in the list
+  __shared__ int wcnt[kDeriveThreads / 64][kClasses];
+  const int g = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const GroupDesc d = group_desc(a, w, g);
+  const int padded = w.s_size[g];
+  if (padded == 0) return;
+  const int64_t base = w.s_off[g];
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int c = 0; c < kClasses; ++c) {
+      cbase[c] = acc;
+      acc += w.s_cnt[g * kClasses + c];
+    }
+  }
+  __syncthreads();
+  for (int i0 = 0; i0 < d.cnt; i0 += kDeriveThreads) {
+    const int i = i0 + threadIdx.x;
+    int k = 0, c = -1;
+    uint32_t m = 0;
+    if (i < d.cnt) {
+      k = a.kv_idx[d.off + i];
+      m = a.kv_mask[d.off + i];
+      c = ste_class(a, d, k, m);
+      if (c >= kClasses) c = -1;
+    }
+    for (int cc = lane; cc < kClasses; cc += 64) wcnt[wave][cc] = 0;
+    // rank inside the wave: one ballot per distinct class present
+    int rank = 0;
+    uint64_t rem = __ballot(c >= 0);
+    while (rem) {
+      const int leader = __ffsll((unsigned long long)rem) - 1;
+      const int cl = __shfl(c, leader);
+      const uint64_t same = __ballot(c == cl);
+      if (c == cl) rank = __popcll(same & ((1ull << lane) - 1));
+      if (lane == 0) wcnt[wave][cl] = __popcll(same);
+      rem &= ~same;
+    }
+    __syncthreads();
+    if (c >= 0) {
+      int before = 0;
+      for (int v = 0; v < wave; ++v) before += wcnt[v][c];
+      const int64_t pos = base + cbase[c] + before + rank;
+      a.ste_kv_idx[pos] = k;
+      a.ste_kv_mask[pos] = m;
+      a.ste_kv_class[pos] = c;
+    }
+    __syncthreads();
+    for (int cc = threadIdx.x; cc < kClasses; cc += blockDim.x) {
+      int n = 0;
+      for (int v = 0; v < kDeriveThreads / 64; ++v) n += wcnt[v][cc];
+      cbase[cc] += n;
+    }
+    __syncthreads();
+  }
+  int n = 0;
+  for (int c = 0; c < kClasses; ++c) n += w.s_cnt[g * kClasses + c];
+  for (int p = n + threadIdx.x; p < padded; p += blockDim.x) {
+    a.ste_kv_idx[base + p] = 0;
+    a.ste_kv_mask[base + p] = 0;
+    a.ste_kv_class[base + p] = 0;
+  }
+  // the group's STE items
+  const int first = w.grp_first[g], end = w.grp_first[g + 1];
+  for (int i = first + threadIdx.x; i < end; i += blockDim.x) {
+    const int64_t o = w.s_item_off[g] + (i - first);
+    for (int e = 0; e < 8; ++e) a.ste_items[8 * o + e] = a.items[8 * (int64_t)i + e];
+    a.ste_items[8 * o + 5] = (int32_t)base;
+    a.ste_items[8 * o + 6] = padded;
+  }
+}
+
+// Key-major items: the forward items with their group's list offset / size.
+__global__ void derive_key_items_kernel(HierDeriveArgs a, DeriveWs w) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.n_items) return;
+  const int g = w.grp_of_item[i];
+  for (int e = 0; e < 8; ++e) a.key_items[8 * (int64_t)i + e] = a.items[8 * (int64_t)i + e];
+  a.key_items[8 * (int64_t)i + 5] = (int32_t)w.t_off[g];
+  a.key_items[8 * (int64_t)i + 6] = w.t_size[g];
+}
+
+// AND of the masks of every 64 entries (one wave per tile).
+__global__ void derive_blk_and_kernel(const uint32_t* mask, uint32_t* blk, int64_t n_tiles) {
+  const int64_t tile = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (tile >= n_tiles) return;
+  uint32_t v = mask[tile * 64 + (threadIdx.x & 63)];
+  for (int s = 32; s >= 1; s >>= 1) v &= __shfl_xor(v, s);
+  if ((threadIdx.x & 63) == 0) blk[tile] = v;
+}
+
+int derive_validate(const HierDeriveArgs* a, DeriveWs* w) {
+  HIER_REQUIRE(a != nullptr, HIER_EINVAL, "args is NULL");
+  HIER_REQUIRE(a->n_items >= 1 && a->n_groups >= 1 && a->rows >= 1 && a->nq_max >= 1 &&
+                   a->nq_max <= 32,
+               HIER_EINVAL, "invalid n_items=%d n_groups=%d rows=%d nq_max=%d", a->n_items,
+               a->n_groups, a->rows, a->nq_max);
+  HIER_REQUIRE((int64_t)a->n_groups * a->n_groups * a->nq_max <= kMaxTable, HIER_EUNSUPPORTED,
+               "too many groups for the device transposer (%d groups x %d frames)", a->n_groups,
+               a->nq_max);
+  HIER_REQUIRE(a->kv_len >= 0, HIER_EINVAL, "invalid kv_len=%d", a->kv_len);
+  HIER_REQUIRE(a->P >= 0 && a->T >= 0 && a->L >= 0 && a->N >= 0 && a->KL >= 0, HIER_EINVAL,
+               "invalid STE geometry");
+  HIER_REQUIRE(a->items && a->kv_idx && a->kv_mask && a->totals && a->ws, HIER_EINVAL,
+               "NULL input pointer");
+  const int64_t need = derive_ws_layout(*a, w);
+  HIER_REQUIRE(a->ws_bytes >= need, HIER_EINVAL, "workspace holds %lld bytes, %lld needed",
+               (long long)a->ws_bytes, (long long)need);
+  return HIER_OK;
+}
+
+void fill(int32_t* p, int64_t n, int32_t v, hipStream_t s) {
+  const int grid = (int)std::min<int64_t>((n + 255) / 256, 4096);
+  if (grid > 0) hipLaunchKernelGGL(derive_fill_kernel, dim3(grid), dim3(256), 0, s, p, n, v);
+}
+
+}  // namespace
+
+extern "C" int64_t hier_derive_workspace(const HierDeriveArgs* args) {
+  if (!args) return -1;
+  HierDeriveArgs a = *args;
+  a.ws = nullptr;
+  return derive_ws_layout(a, nullptr);
+}
+
+extern "C" int hier_derive_count(const HierDeriveArgs* args, void* stream) {
+  hier::clear_error();
+  DeriveWs w;
+  int rc = derive_validate(args, &w);
+  if (rc) return rc;
+  const HierDeriveArgs& a = *args;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t tab = (int64_t)a.n_groups * a.n_groups * a.nq_max;
+  fill(w.grp_first, (int64_t)a.n_groups + 1, 0, s);
+  fill(w.tok_g, a.rows, -1, s);
+  fill(reinterpret_cast<int32_t*>(w.table), tab, 0, s);
+  fill(w.runs, tab, 0, s);
+  hipLaunchKernelGGL(derive_groups_kernel, dim3(1), dim3(kScanThreads), 0, s, a, w);
+  hipLaunchKernelGGL(derive_tokens_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
+  hipLaunchKernelGGL(derive_runs_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
+  hipLaunchKernelGGL(derive_key_sizes_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
+  hipLaunchKernelGGL(derive_ste_count_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
+  hipLaunchKernelGGL(derive_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a, w);
+  return hier::check_launch("derive count kernels");
+}
+
+extern "C" int hier_derive_build(const HierDeriveArgs* args, void* stream) {
+  hier::clear_error();
+  DeriveWs w;
+  int rc = derive_validate(args, &w);
+  if (rc) return rc;
+  const HierDeriveArgs& a = *args;
+  HIER_REQUIRE(a.key_items && a.key_q_idx && a.key_q_mask && a.key_blk_and, HIER_EINVAL,
+               "key-major output pointer is NULL");
+  HIER_REQUIRE(a.key_entries >= 0 && a.key_entries % kTileKeys == 0 && a.ste_entries >= 0 &&
+                   a.ste_entries % kTileKeys == 0,
+               HIER_EINVAL, "list sizes must be the multiples of 64 that pass 1 returned");
+  const bool ste = a.ste_entries > 0;
+  if (ste)
+    HIER_REQUIRE(a.ste_items && a.ste_kv_idx && a.ste_kv_mask && a.ste_blk_and && a.ste_kv_class,
+                 HIER_EINVAL, "STE output pointer is NULL");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(derive_key_write_kernel, dim3(a.n_groups), dim3(kScanThreads), 0, s, a, w);
+  hipLaunchKernelGGL(derive_key_items_kernel, dim3((a.n_items + 255) / 256), dim3(256), 0, s, a,
+                     w);
+  const int64_t kt = a.key_entries / kTileKeys;
+  if (kt > 0)
+    hipLaunchKernelGGL(derive_blk_and_kernel, dim3((unsigned)((kt + 3) / 4)), dim3(256), 0, s,
+                       a.key_q_mask, a.key_blk_and, kt);
+  if (ste) {
+    hipLaunchKernelGGL(derive_ste_write_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a,
+                       w);
+    const int64_t st = a.ste_entries / kTileKeys;
+    hipLaunchKernelGGL(derive_blk_and_kernel, dim3((unsigned)((st + 3) / 4)), dim3(256), 0, s,
+                       a.ste_kv_mask, a.ste_blk_and, st);
+  }
+  return hier::check_launch("derive build kernels");
 }

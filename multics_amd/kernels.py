@@ -17,7 +17,7 @@ import torch
 
 from . import _capi
 from . import metadata as M
-from .metadata import HierTiledBlockLayout, TileList, ste_tiles, transpose_tiles
+from .metadata import HierTiledBlockLayout, TileList, backward_lists
 
 
 def _stream(dev) -> C.c_void_p:
@@ -131,19 +131,23 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     if lse.dtype != torch.float32 or lse.dim() != 2 or lse.shape[0] != H or \
             lse.shape[1] < tiles.row_extent or lse.stride(1) != 1:
         raise ValueError("lse must be fp32 [H, >=rows] with unit row stride")
-    kt = key_tiles if key_tiles is not None else transpose_tiles(tiles)
+    ste = None
+    if ste_geometry is not None:
+        P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
+        if max(P_, N_) > STE_CLASSES:
+            raise NotImplementedError(f"membership STE supports up to {STE_CLASSES} players / groups")
+    if key_tiles is not None and ste_geometry is None:
+        kt = key_tiles
+    else:
+        kt, ste = backward_lists(tiles, ste_geometry)
+        kt = key_tiles if key_tiles is not None else kt
     dev = q.device
     dq = torch.zeros_like(q3)
     dk = torch.zeros_like(k3)
     dv = torch.zeros_like(v3)
     ws = None if no_alloc_workspace else \
         torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
-    ste = None
     if ste_geometry is not None:
-        P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
-        if max(P_, N_) > STE_CLASSES:
-            raise NotImplementedError(f"membership STE supports up to {STE_CLASSES} players / groups")
-        ste = ste_tiles(tiles, P=P_, T=T_, L=L_, N=N_, KL=KL_)
         partial = torch.zeros((H, tiles.row_extent, STE_CLASSES), dtype=torch.float32, device=dev)
     args = _capi.HierBwdArgs(
         H=H, D=D, n_items=tiles.n_items, n_key_items=kt.n_items,

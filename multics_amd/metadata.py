@@ -58,6 +58,7 @@ class TileList:
     key_extent: int = 0          # 1 + largest K/V row index any key can address
     row_extent: int = 0          # 1 + largest Q/O row index any item can address
     rows_per_item: int = ROWS_PER_ITEM
+    frames_per_group: int = 0    # query frames of every (block, stream) group; 0 = unknown
 
 
 @dataclass(frozen=True)
@@ -545,7 +546,7 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     tiles = TileList(items=items[:n_items], kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
                      n_items=n_items, item_ranges=ranges, logical_pairs=int(pairs.sum()),
                      key_extent=int(key_ext), row_extent=int(row_ext),
-                     rows_per_item=rows_per_item)
+                     rows_per_item=rows_per_item, frames_per_group=int(n))
     tiles._keepalive = (dv, keep)  # device inputs must outlive the async build
     layouts = None
     if tiled_res is not None:
@@ -558,9 +559,11 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
 # key-major (transposed) tile list for the backward
 # --------------------------------------------------------------------------
 
-def transpose_tiles(tiles: TileList) -> TileList:
+def transpose_tiles_host(tiles: TileList) -> TileList:
     """Key-major counterpart of a full-sequence tile list (dK / dV pass of
-    ``hier_attn_bwd``).
+    ``hier_attn_bwd``), built on the host: the specification of the device
+    builder ``hier_derive_*`` (``backward_lists``), which must equal it bit
+    for bit.
 
     In a full-sequence topology every token is a query row of exactly one
     (block, stream) group and a key of the same group; the forward list of a
@@ -570,12 +573,8 @@ def transpose_tiles(tiles: TileList) -> TileList:
     of its key frames, each with a bitmask over the group's key frames: items
     keep the forward items' row descriptors (now key rows), the lists hold
     query rows.  Query units are ordered by (query group, query frame); lists
-    are padded to 64 rows with (row 0, mask 0).  Built on the host from the
-    device list once per topology and cached on ``tiles``.
+    are padded to 64 rows with (row 0, mask 0).
     """
-    cached = getattr(tiles, "_transposed", None)
-    if cached is not None:
-        return cached
     dev = tiles.items.device
     items = tiles.items[:tiles.n_items].cpu().numpy().astype(np.int64)
     kv_idx = tiles.kv_idx.cpu().numpy().astype(np.int64)
@@ -665,11 +664,10 @@ def transpose_tiles(tiles: TileList) -> TileList:
                    n_items=tiles.n_items, item_ranges=tiles.item_ranges,
                    logical_pairs=pairs, key_extent=tiles.row_extent, row_extent=tiles.key_extent,
                    rows_per_item=tiles.rows_per_item)
-    tiles._transposed = out
     return out
 
 
-def ste_tiles(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
+def ste_tiles_host(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
     """Query-major list of the membership-gated edges of a full-sequence tile
     list (the membership STE pass of ``hier_attn_bwd``).
 
@@ -680,12 +678,8 @@ def ste_tiles(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
     its local-hub keys and, per local-hub group, its player keys, with the
     forward masks and per key the class (g for player rows, p for hub rows);
     other groups are dropped.  Returns ``(TileList, kv_class)`` or None when no
-    edge is gated; cached on ``tiles``.
+    edge is gated.  Host specification of the device builder (``backward_lists``).
     """
-    key = (P, T, L, N, KL)
-    cache = getattr(tiles, "_ste", None)
-    if cache is not None and cache[0] == key:
-        return cache[1]
     a0, g0 = P * T * L, P * T * L + T * N * KL
     dev = tiles.items.device
     items = tiles.items[:tiles.n_items].cpu().numpy().astype(np.int64)
@@ -736,8 +730,109 @@ def ste_tiles(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
                        key_extent=tiles.key_extent, row_extent=tiles.row_extent,
                        rows_per_item=tiles.rows_per_item)
         res = (lst, to_dev(np.concatenate(cls_parts)))
-    tiles._ste = (key, res)
     return res
+
+
+_DERIVE_ERRORS = ((1, "a token is a query row of two groups"),
+                  (2, "a key is not a query row of any group"),
+                  (4, "key lists are not whole key frames"),
+                  (8, "the work items are not grouped by key list"),
+                  (16, "a list offset does not fit in 32 bits"))
+
+
+def _groups_and_frames(tiles: TileList):
+    if tiles.item_ranges and tiles.frames_per_group:
+        return sum(len(b) for b in tiles.item_ranges), int(tiles.frames_per_group)
+    it = tiles.items[:tiles.n_items].cpu().numpy()
+    return int((it[:, 3] == 0).sum()), int(it[:, 7].max(initial=1))
+
+
+def _derive_device(tiles: TileList, ste_geometry):
+    """Both backward lists of a device tile list with the ``hier_derive_*``
+    kernels (two passes, one read-back of the totals in between)."""
+    dev = tiles.items.device
+    ng, nq = _groups_and_frames(tiles)
+    P, T, L, N, KL = (int(x) for x in ste_geometry) if ste_geometry is not None else (0,) * 5
+    a = _capi.HierDeriveArgs(n_items=tiles.n_items, n_groups=ng, rows=int(tiles.row_extent),
+                             nq_max=nq, kv_len=int(tiles.kv_idx.numel()), P=P, T=T, L=L, N=N,
+                             KL=KL, items=tiles.items.data_ptr(), kv_idx=tiles.kv_idx.data_ptr(),
+                             kv_mask=tiles.kv_mask.data_ptr())
+    ws_bytes = int(_capi.lib().hier_derive_workspace(C.byref(a)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    totals = torch.zeros(8, dtype=torch.int64, device=dev)
+    a.ws, a.ws_bytes, a.totals = ws.data_ptr(), ws_bytes, totals.data_ptr()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _capi.call("hier_derive_count", C.byref(a), stream)
+    n_key, pairs, n_ste, n_ste_items, err = (int(x) for x in totals[:5].cpu())
+    for bit, msg in _DERIVE_ERRORS:
+        if err & bit:
+            raise AssertionError(f"transpose_tiles: {msg}")
+    if pairs != tiles.logical_pairs:
+        raise AssertionError(f"transpose_tiles: {pairs} pairs, forward list has {tiles.logical_pairs}")
+    i32 = dict(dtype=torch.int32, device=dev)
+    k_items = torch.empty((tiles.n_items, 8), **i32)
+    k_idx = torch.zeros(max(n_key, 1), **i32)
+    k_mask = torch.zeros(max(n_key, 1), **i32)
+    k_blk = torch.zeros(max(n_key // TILE_KEYS, 1), **i32)
+    a.key_entries, a.ste_entries = n_key, (n_ste if n_ste_items > 0 else 0)
+    a.key_items, a.key_q_idx = k_items.data_ptr(), k_idx.data_ptr()
+    a.key_q_mask, a.key_blk_and = k_mask.data_ptr(), k_blk.data_ptr()
+    if n_ste_items > 0:
+        s_items = torch.empty((n_ste_items, 8), **i32)
+        s_idx, s_mask, s_cls = (torch.empty(n_ste, **i32) for _ in range(3))
+        s_blk = torch.empty(n_ste // TILE_KEYS, **i32)
+        a.ste_items, a.ste_kv_idx, a.ste_kv_mask = (s_items.data_ptr(), s_idx.data_ptr(),
+                                                    s_mask.data_ptr())
+        a.ste_blk_and, a.ste_kv_class = s_blk.data_ptr(), s_cls.data_ptr()
+    _capi.call("hier_derive_build", C.byref(a), stream)
+    kt = TileList(items=k_items, kv_idx=k_idx, kv_mask=k_mask, blk_and=k_blk,
+                  n_items=tiles.n_items, item_ranges=tiles.item_ranges, logical_pairs=pairs,
+                  key_extent=tiles.row_extent, row_extent=tiles.key_extent,
+                  rows_per_item=tiles.rows_per_item)
+    ste = None
+    if n_ste_items > 0:
+        lst = TileList(items=s_items, kv_idx=s_idx, kv_mask=s_mask, blk_and=s_blk,
+                       n_items=n_ste_items, item_ranges=(), logical_pairs=0,
+                       key_extent=tiles.key_extent, row_extent=tiles.row_extent,
+                       rows_per_item=tiles.rows_per_item)
+        ste = (lst, s_cls)
+    kt._keepalive = (ws, totals)
+    return kt, ste
+
+
+def backward_lists(tiles: TileList, ste_geometry=None):
+    """``(key-major list, STE list)`` of a full-sequence tile list for the
+    backward, the STE list ``(TileList, kv_class)`` or None (no geometry, or no
+    gated edge).  Device lists are derived on the GPU by the ``hier_derive_*``
+    kernels, bit for bit the host builders ``transpose_tiles_host`` /
+    ``ste_tiles_host``, which serve host lists.  Cached on ``tiles`` per STE
+    geometry."""
+    key = None if ste_geometry is None else tuple(int(x) for x in ste_geometry)
+    cache = tiles.__dict__.setdefault("_derived", {})
+    hit = cache.get(key)
+    if hit is not None:
+        return hit
+    if tiles.items.is_cuda:
+        res = _derive_device(tiles, key)
+    else:
+        kt = next(iter(cache.values()))[0] if cache else transpose_tiles_host(tiles)
+        ste = None if key is None else ste_tiles_host(tiles, P=key[0], T=key[1], L=key[2],
+                                                      N=key[3], KL=key[4])
+        res = (kt, ste)
+    cache[key] = res
+    return res
+
+
+def transpose_tiles(tiles: TileList) -> TileList:
+    """Key-major list of ``tiles`` (see ``backward_lists``), cached on it."""
+    for (kt, _) in getattr(tiles, "_derived", {}).values():
+        return kt
+    return backward_lists(tiles)[0]
+
+
+def ste_tiles(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
+    """STE list of ``tiles`` (see ``backward_lists``), cached on it."""
+    return backward_lists(tiles, (P, T, L, N, KL))[1]
 
 
 # --------------------------------------------------------------------------

@@ -22,12 +22,13 @@ STRUCTS = {
     "HierBwdArgs": _capi.HierBwdArgs,
     "HierPageArgs": _capi.HierPageArgs,
     "HierFrameAttnArgs": _capi.HierFrameAttnArgs,
+    "HierDeriveArgs": _capi.HierDeriveArgs,
 }
 
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(hier_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(hier_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():

@@ -1,0 +1,114 @@
+"""The backward's key-major and membership-STE lists built on the GPU
+(``hier_derive_count`` / ``hier_derive_build`` in csrc/hier_meta.hip) equal
+the host builders ``metadata.transpose_tiles_host`` / ``ste_tiles_host`` bit
+for bit: items, row / key indices, masks, per-64 ANDs, classes, pair count.
+
+Cases: every bench topology that has a full-sequence tile list (C2 fixed
+groups, P6 pairs, C3 per-frame dynamic groups, P10 random blocks, C5 soft
+membership logits), a membership form with orphans, a no-local-hub form and a
+small labels form with an inactive group; plus a list with one key of a frame
+dropped, which both builders refuse (the device kernels flag it and the host
+side raises).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from multics_amd import metadata as M
+from tests.gpu_util import need_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+
+def _same(a: torch.Tensor, b: torch.Tensor, what: str):
+    a, b = a.detach().cpu(), b.detach().cpu()
+    assert a.dtype == b.dtype and a.shape == b.shape, (what, a.dtype, b.dtype, a.shape, b.shape)
+    assert torch.equal(a, b), what
+
+
+def _check_lists(tiles, geom):
+    dev_kt, dev_ste = M._derive_device(tiles, geom)
+    torch.cuda.synchronize()
+    host_kt = M.transpose_tiles_host(tiles)
+    for f in ("items", "kv_idx", "kv_mask", "blk_and"):
+        _same(getattr(dev_kt, f), getattr(host_kt, f), f"key-major {f}")
+    for f in ("n_items", "logical_pairs", "key_extent", "row_extent", "rows_per_item"):
+        assert getattr(dev_kt, f) == getattr(host_kt, f), f
+    if geom is None:
+        assert dev_ste is None
+        return
+    host_ste = M.ste_tiles_host(tiles, P=geom[0], T=geom[1], L=geom[2], N=geom[3], KL=geom[4])
+    assert (dev_ste is None) == (host_ste is None)
+    if host_ste is None:
+        return
+    (dl, dc), (hl, hc) = dev_ste, host_ste
+    for f in ("items", "kv_idx", "kv_mask", "blk_and"):
+        _same(getattr(dl, f), getattr(hl, f), f"STE {f}")
+    _same(dc, hc, "STE classes")
+    assert dl.n_items == hl.n_items
+
+
+@pytest.mark.parametrize("cfg", ["c2", "p6", "c3", "p10", "c5"])
+def test_device_lists_match_host_at_bench_sizes(cfg):
+    need_gpu()
+    dev = torch.device("cuda", 0)
+    say(f"derive {cfg}")
+    P, T, L, N, KL, KG, n, W, H, D, grp = bench.CONFIGS[cfg]
+    _, tiles, _, _ = bench.build_case(cfg, dev)
+    _check_lists(tiles, (P, T, L, N, KL))
+    # backward_lists routes device lists through the device builder and caches
+    kt, ste = M.backward_lists(tiles, (P, T, L, N, KL))
+    assert M.backward_lists(tiles, (P, T, L, N, KL))[0] is kt
+    assert M.transpose_tiles(tiles) is kt
+
+
+@pytest.mark.parametrize("kind", ["membership", "no_local", "labels_inactive"])
+def test_device_lists_match_host_small(kind):
+    need_gpu()
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(7)
+    P, T, L, N, KL, KG, n, W = 4, 6, 24, 3, 2, 3, 3, 4
+    labels = active = mem = go = None
+    no_local = False
+    if kind == "membership":
+        mem = rng.random((T, N, P)) < 0.35
+        go = ~mem.any(1)
+        go[0, 0] = False                               # an orphan: no group, not global-only
+    elif kind == "no_local":
+        mem = rng.random((T, N, P)) < 0.5
+        go = ~mem.any(1)
+        KL, no_local = 0, True
+    else:
+        labels = rng.integers(0, N, size=(T, P))
+        active = np.zeros((T, N), dtype=bool)
+        active[np.arange(T)[:, None], labels] = True
+        active[:, -1] = False
+    say(f"derive small {kind}")
+    tiles = M.full_sequence_tiles(device=dev, P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                  direct=True, labels=labels, active=active, membership=mem,
+                                  global_only=go, no_local=no_local)
+    _check_lists(tiles, (P, T, L, N, KL))
+    _check_lists(tiles, None)
+
+
+def test_device_builder_refuses_partial_frames():
+    need_gpu()
+    dev = torch.device("cuda", 0)
+    P, T, L, N, KL, KG, n, W = 2, 3, 8, 2, 1, 1, 3, -1
+    tiles = M.full_sequence_tiles(device=dev, P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                  direct=True, labels=np.zeros((T, P), int),
+                                  active=np.ones((T, N), bool))
+    m = tiles.kv_mask.clone()
+    live = torch.nonzero(m.cpu()).flatten()
+    m[int(live[1])] = 0                                  # drop the second key of a frame
+    bad = M.TileList(items=tiles.items, kv_idx=tiles.kv_idx, kv_mask=m, blk_and=tiles.blk_and,
+                     n_items=tiles.n_items, item_ranges=tiles.item_ranges,
+                     logical_pairs=tiles.logical_pairs, key_extent=tiles.key_extent,
+                     row_extent=tiles.row_extent, frames_per_group=tiles.frames_per_group)
+    say("derive refuses a partial frame")
+    with pytest.raises(AssertionError, match="whole key frames"):
+        M._derive_device(bad, None)
+    with pytest.raises(AssertionError):
+        M.transpose_tiles_host(bad)
