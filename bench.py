@@ -303,6 +303,59 @@ def bench_training(dev, steps=10, warmup=3):
                     "flipped membership must"}
 
 
+def bench_layer(dev, steps=10, warmup=3):
+    """C2 through the drop-in module: ``SelfAttention.forward(x, freqs, mask,
+    cam_tokens)`` (attention.py:436-442 signature) under no_grad, with the
+    block mask of ``build_stage2_hier_flex_block_mask``: the q / k / v GEMMs,
+    the fused camera + RMSNorm + RoPE prologue on q and k, the attention
+    (V read in place from the v projection) and the o-projection.  Random
+    bf16 weights, camera adapter on (random weights, no dropout), camera12 of
+    seeded poses, the simplex RoPE table.  The GEMMs are also timed alone on
+    the same shapes."""
+    import torch.nn.functional as F
+    from multics_amd import rope
+    from multics_amd.hier_masks import build_stage2_hier_flex_block_mask
+    from multics_amd.module import SelfAttention
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS["c2"]
+    dim = H * D
+    labels, _, _ = grouping(grp, P, T, N, np.random.default_rng(SEED))
+    torch.manual_seed(SEED)
+    layer = SelfAttention(dim, H).to(device=dev, dtype=torch.bfloat16).eval()
+    layer.num_frame_per_block, layer.local_attn_size = n, W
+    layer.enable_camera_pose_qk(12, dropout_p=0.0)
+    with torch.no_grad():
+        layer.cam_q.weight.normal_(0.0, 0.02)
+        layer.cam_k.weight.normal_(0.0, 0.02)
+    lab = torch.from_numpy(np.asarray(labels)).long()
+    mask, S, _ = build_stage2_hier_flex_block_mask(P, T, L, N, KL, KG, n, W, lab, None, True, dev)
+    h, w = (11, 20) if L == 220 else (1, L)
+    bands = rope.precompute_freqs_cis_4d_wan_rerope(D)
+    verts = rope.build_simplex_vertices(10, rope.WAN_REROPE_SPLITS[1])
+    freqs = rope.build_self_attn_freqs_with_hub(bands, verts, T, h, w, "cpu", list(range(P)),
+                                                N * KL + KG).to(dev)
+    cam = camera_tokens(P, T, L, N * KL + KG, dev)[None]
+    x = torch.randn(1, S, dim, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        ms_layer = float(np.median(time_events(lambda: layer(x, freqs, mask, cam_tokens=cam),
+                                               steps, warmup)))
+
+        def gemms():
+            for lin in (layer.q, layer.k, layer.v, layer.o):
+                F.linear(x, lin.weight, lin.bias)
+
+        ms_gemm = float(np.median(time_events(gemms, steps, warmup)))
+    E = mask.tiles.logical_pairs
+    flop_gemm = 8.0 * S * dim * dim
+    flop_attn = 4.0 * H * D * E
+    return {"tokens": S, "dim": dim, "ms_layer": round(ms_layer, 4),
+            "ms_gemms_qkvo": round(ms_gemm, 4),
+            "ms_rest": round(ms_layer - ms_gemm, 4),
+            "tflops_layer": round((flop_gemm + flop_attn) / (ms_layer * 1e-3) / 1e12, 1),
+            "note": "module forward under no_grad (GEMMs + fused q/k prologue + attention + "
+                    "o-projection); ms_rest = layer - the four GEMMs alone (prologue, "
+                    "attention, the cos/sin table, the output buffer); GEMM FLOP 8*S*dim^2"}
+
+
 def bench_rollout(dev, passes=10):
     """Config C4: cached rollout, 10 players, chunk = 6 latent frames = 2 blocks
     of 3 through the paged KV cache; time one denoising pass over a chunk in
@@ -496,8 +549,9 @@ def main():
 
     g = torch.Generator(device=dev).manual_seed(SEED)
     mk = lambda: (torch.randn(H, S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
-    qh, kh, vh = mk(), mk(), mk()
-    q, k, v = (t.permute(1, 0, 2) for t in (qh, kh, vh))       # [S,H,D] views, head-major storage
+    # token-major [S, H, D], the layout the module's no-grad path feeds the
+    # kernel (prologue q / k, the v projection in place)
+    q, k, v = (mk().permute(1, 0, 2).contiguous() for _ in range(3))
     out = torch.empty(S, H, D, dtype=torch.bfloat16, device=dev)
 
     def step():
@@ -514,15 +568,14 @@ def main():
     dim = H * D
     qx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
     kx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
-    vx = (torch.randn(S, dim, generator=g, device=dev)).to(torch.bfloat16)
     cam = camera_tokens(P, T, L, N * KL + KG, dev)
     wcq = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
     wck = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
     nw = torch.ones(dim, dtype=torch.bfloat16, device=dev)
     cs, sn = rope_tables(P, T, L, N * KL + KG, D, dev)
-    pro = time_events(lambda: qkv_prologue(qx, kx, vx, norm_q_w=nw, norm_k_w=nw, rope_cos=cs,
+    pro = time_events(lambda: qkv_prologue(qx, kx, None, norm_q_w=nw, norm_k_w=nw, rope_cos=cs,
                                            rope_sin=sn, num_heads=H, eps=1e-6, cam=cam,
-                                           w_cam_q=wcq, w_cam_k=wck, out_layout="hsd"),
+                                           w_cam_q=wcq, w_cam_k=wck, out_layout="shd"),
                       max(args.steps // 5, 3), 2)
     pro_ms = float(np.median(pro))
 
@@ -571,6 +624,7 @@ def main():
         for cfg in ("p6", "c3", "p10"):
             if cfg != args.config:
                 suite[f"fwd_{cfg}"] = bench_forward_cfg(cfg, dev)
+        suite["layer_c2"] = bench_layer(dev)
         suite["training_c5"] = bench_training(dev)
         suite["rollout_c4"] = bench_rollout(dev)
         suite["rollout_c4_cfg"] = bench_rollout_cfg(dev)

@@ -14,12 +14,15 @@
 // result can differ from the reference by one bf16 ulp.  The RMS spans all
 // heads (the full model dim), so one workgroup owns whole tokens of one
 // projection (q or k): dim/CPT threads x CPT channels (CPT = 4 up to dim 3072,
-// else 8).  Camera weights stay in registers, packed, and the workgroup's
-// camera rows in LDS, while the workgroup walks kTokens tokens two at a time:
-// one workgroup reduction serves both tokens, each packed weight pair feeds
-// both (v_dot2_f32_bf16), and the next two tokens' projections are loaded
-// while the current two are computed.  The q workgroups also copy V into the
-// requested layout.
+// else 8).  The workgroup walks kTokens tokens two at a time: one workgroup
+// reduction (DPP and lane swaps inside each wave, one LDS barrier across
+// waves) serves both tokens, and the next two tokens' projections and RoPE
+// rows are loaded into a second register set while the current two are
+// computed.  A token's camera row is the same for every token of a player's
+// frame (zero for hub tokens), so the camera product (v_dot2_f32_bf16 over
+// packed bf16 pairs, weights read when needed) is recomputed only where the
+// row changes.  With v_out the q workgroups also copy V into the requested
+// layout.
 #include "hier_common.h"
 
 namespace {
@@ -28,34 +31,89 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kTokens = 32;
+constexpr int kTrip = 2;     // tokens per trip of the token loop
 
 __device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 __device__ __forceinline__ uint32_t f2bf(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// Both values rounded to bf16 (round to nearest even) and back: one
+// v_cvt_pk_bf16_f32 for the pair, then a shift and a mask.
+__device__ __forceinline__ void rbf2(float& a, float& b) {
+  const f32x2 v = {a, b};
+  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  a = __uint_as_float(u << 16);
+  b = __uint_as_float(u & 0xffff0000u);
+}
 
-// Sums of NV values over the workgroup (blockDim a multiple of 64 or a power
-// of two below 64); red holds 16 waves x NV partial sums.
+// Sum over the 64 lanes of a wave, left in every lane: DPP within rows of
+// 16, then the row swaps of gfx950 (v_permlane16_swap, v_permlane32_swap).
+__device__ __forceinline__ float dpp_add(float v, int ctrl_sel) {
+  int u;
+  switch (ctrl_sel) {
+    case 0: u = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false); break;
+    case 1: u = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false); break;
+    case 2: u = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false); break;
+    default: u = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false); break;
+  }
+  return v + __int_as_float(u);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = dpp_add(v, 0);   // quad_perm [1,0,3,2]
+  v = dpp_add(v, 1);   // quad_perm [2,3,0,1]
+  v = dpp_add(v, 2);   // row_ror:4
+  v = dpp_add(v, 3);   // row_ror:8
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations,
+// not for its outstanding global loads (__syncthreads' workgroup fence would
+// wait for those too, so that the next trip's prefetched projections would
+// land before the barrier instead of during the trip).
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Sums of NV values over the workgroup.  Full waves (blockDim a multiple of
+// 64): a register reduction per wave, then the wave sums through red, laid
+// out [parity][NV][16 waves] with the slots of absent waves zero (the caller
+// clears red once), so every value reads 16 slots unconditionally.  The two
+// parity buffers alternate between calls, so one barrier per call suffices:
+// the buffer a call writes was last read before the previous call's barrier.
+// Below 64 threads (one partial wave): a shuffle reduction.
 template <int NV>
-__device__ __forceinline__ void block_sum(float* v, float* red) {
-  const int width = blockDim.x < 64 ? (int)blockDim.x : 64;
-  for (int d = 1; d < width; d <<= 1)
+__device__ __forceinline__ void block_sum(float* v, float* red, int parity) {
+  if (blockDim.x >= 64) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = wave_sum(v[i]);
+    float* r = red + parity * 16 * NV;
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+      for (int i = 0; i < NV; ++i) r[i * 16 + (threadIdx.x >> 6)] = v[i];
+    barrier_lds();
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const float4* r4 = reinterpret_cast<const float4*>(r + i * 16);
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 w = r4[j];
+        t += (w.x + w.y) + (w.z + w.w);
+      }
+      v[i] = t;
+    }
+    return;
+  }
+  for (int d = 1; d < (int)blockDim.x; d <<= 1)
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] += __shfl_xor(v[i], d, 64);
-  const int nw = (blockDim.x + 63) >> 6;
-  const int w = threadIdx.x >> 6;
-  __syncthreads();   // the previous sums have been read
-  if ((threadIdx.x & 63) == 0)
-#pragma unroll
-    for (int i = 0; i < NV; ++i) red[w * NV + i] = v[i];
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    float t = 0.f;
-    for (int ww = 0; ww < nw; ++ww) t += red[ww * NV + i];
-    v[i] = t;
-  }
 }
 
 // CPT channels per thread: 4 for model dims up to 3072, 8 up to 4096.
@@ -69,16 +127,18 @@ struct Chw<8> { typedef u32x4 type; };
 // blockIdx.y selects the projection: 0 = q (and the V copy), 1 = k.  Keeping
 // the two on separate workgroups halves the camera weights each thread holds,
 // which lets two workgroups share a CU.
-template <int C, int kCPT>
+template <int C, int kCPT, bool kCopyV>
 __global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPrologueArgs a) {
   typedef typename Chw<kCPT>::type chw_t;
+  typedef float rope_t __attribute__((ext_vector_type(kCPT / 2)));
   constexpr int CW = C > 0 ? C / 2 : 1;          // packed camera words per token
-  __shared__ float red[16 * 2];
+  __shared__ __align__(16) float red[2 * 16 * kTrip];
   __shared__ uint32_t camw[kTokens * CW];        // this workgroup's camera rows
+  __shared__ uint8_t cam_new[kTokens];           // row differs from the previous token's
   const bool is_k = blockIdx.y != 0;
   const uint16_t* const xin = is_k ? a.kx : a.qx;
   uint16_t* const out = is_k ? a.k_out : a.q_out;
-  const bool copy_v = !is_k && a.v_out != nullptr;
+  const bool copy_v = kCopyV && !is_k;
   const int dim = a.H * a.D;
   const int c0 = threadIdx.x * kCPT;        // first channel of this thread
   const int head = c0 / a.D, d0 = c0 - head * a.D;
@@ -86,16 +146,9 @@ __global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPro
   const int m0 = d0 / 2;
   const int s_begin = blockIdx.x * kTokens;
   const int s_end = min(a.S, s_begin + kTokens);
-
-  // camera weights of this thread's kCPT channels: rows c0.. of [dim][C] are
-  // contiguous, loaded as packed bf16 pairs (word i = elements 2i, 2i+1)
-  constexpr int NW = C > 0 ? kCPT * C / 8 : 1;     // 16-byte vectors
-  u32x4 wc[NW];
+  const float inv_dim = 1.f / (float)dim;
+  for (int i = threadIdx.x; i < 2 * 16 * kTrip; i += blockDim.x) red[i] = 0.f;
   if constexpr (C > 0) {
-    const uint16_t* const w = is_k ? a.w_cam_k : a.w_cam_q;
-#pragma unroll
-    for (int i = 0; i < NW; ++i)
-      wc[i] = *reinterpret_cast<const u32x4*>(w + (int64_t)c0 * C + 8 * i);
     const uint32_t* src = reinterpret_cast<const uint32_t*>(a.cam + (int64_t)s_begin * C);
     for (int i = threadIdx.x; i < (s_end - s_begin) * CW; i += blockDim.x) camw[i] = src[i];
   }
@@ -104,95 +157,160 @@ __global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPro
     const chw_t g4 = *reinterpret_cast<const chw_t*>((is_k ? a.norm_k_w : a.norm_q_w) + c0);
 #pragma unroll
     for (int e = 0; e < kCPT / 2; ++e) {
-      g[2 * e] = bf2f(g4[e] & 0xffffu);
-      g[2 * e + 1] = bf2f(g4[e] >> 16);
+      g[2 * e] = __uint_as_float(g4[e] << 16);
+      g[2 * e + 1] = __uint_as_float(g4[e] & 0xffff0000u);
     }
   }
-  auto load = [&](int s) { return *reinterpret_cast<const chw_t*>(xin + (int64_t)s * dim + c0); };
-  if constexpr (C > 0) __syncthreads();   // camera rows staged
+  // element offsets of the [S, dim] projections fit in 32 bits (checked by the launcher)
+  auto load = [&](int s) {
+    return *reinterpret_cast<const chw_t*>(xin + (uint32_t)(s * dim + c0));
+  };
+  auto rc = [&](int s) {
+    return *reinterpret_cast<const rope_t*>(a.rope_cos + (uint32_t)(s * half + m0));
+  };
+  auto rs = [&](int s) {
+    return *reinterpret_cast<const rope_t*>(a.rope_sin + (uint32_t)(s * half + m0));
+  };
+  // The camera rows are per frame (all tokens of a player's frame share one,
+  // hub tokens hold zeros), so the camera product of a token is recomputed
+  // only when its row differs from the previous token's, with this thread's
+  // weights (rows c0.. of [dim][C], packed bf16 pairs) read at that point.
+  __syncthreads();   // camera rows staged, red cleared
+  if constexpr (C > 0) {
+    const int t = threadIdx.x;
+    if (t < s_end - s_begin) {
+      bool diff = t == 0;
+      for (int c = 0; c < CW && !diff; ++c) diff = camw[t * CW + c] != camw[(t - 1) * CW + c];
+      cam_new[t] = diff ? 1 : 0;
+    }
+    __syncthreads();
+  }
+  float camp[kCPT];   // bf16-rounded camera product of the last new row
 
-  // Two tokens per trip (one reduction for both, each packed camera weight pair
-  // feeds both), the next two tokens' projections loaded during the current
-  // ones.  An odd last token is paired with itself and stored once.
-  chw_t n0 = load(s_begin), n1 = load(min(s_begin + 1, s_end - 1));
-  for (int s = s_begin; s < s_end; s += 2) {
-    const chw_t x[2] = {n0, n1};
-    const bool second = s + 1 < s_end;
-    const int s1 = second ? s + 1 : s;
-    typedef float rope_t __attribute__((ext_vector_type(kCPT / 2)));
-    rope_t cs[2], sn[2];
-    chw_t v4[2];
-    cs[0] = *reinterpret_cast<const rope_t*>(a.rope_cos + (int64_t)s * half + m0);
-    sn[0] = *reinterpret_cast<const rope_t*>(a.rope_sin + (int64_t)s * half + m0);
-    cs[1] = *reinterpret_cast<const rope_t*>(a.rope_cos + (int64_t)s1 * half + m0);
-    sn[1] = *reinterpret_cast<const rope_t*>(a.rope_sin + (int64_t)s1 * half + m0);
-    if (copy_v) {
-      v4[0] = *reinterpret_cast<const chw_t*>(a.vx + (int64_t)s * dim + c0);
-      v4[1] = *reinterpret_cast<const chw_t*>(a.vx + (int64_t)s1 * dim + c0);
-    }
-    if (s + 2 < s_end) {
-      n0 = load(s + 2);
-      n1 = load(min(s + 3, s_end - 1));
-    }
-    float q[2][kCPT];
+  // kTrip tokens per trip (one reduction for all of them); the next trip's
+  // projections and RoPE rows are loaded during the current one, into the
+  // other of two register sets (no copy between them, so the first use of a
+  // set waits only for its own loads, not for the stores and loads issued
+  // after them).
+  // Past the range's last token a trip repeats it and stores it again.
+  struct Pf {
+    chw_t x[kTrip];
+    rope_t c[kTrip], s[kTrip];
+  };
+  auto fetch = [&](Pf& f, int s) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < kTrip; ++t) {
+      const int st = min(s + t, s_end - 1);
+      f.x[t] = load(st);
+      f.c[t] = rc(st);
+      f.s[t] = rs(st);
+    }
+  };
+  auto trip = [&](int s, int parity, const Pf& use, Pf& nxt) {
+    int sv[kTrip];
+    float cpt[kTrip][kCPT];   // camera product of each token of the trip
 #pragma unroll
-      for (int e = 0; e < kCPT / 2; ++e) {
-        q[t][2 * e] = bf2f(x[t][e] & 0xffffu);
-        q[t][2 * e + 1] = bf2f(x[t][e] >> 16);
-      }
+    for (int t = 0; t < kTrip; ++t) sv[t] = min(s + t, s_end - 1);
+    // the camera products first: a new row's weight loads then wait only for
+    // the previous trip's memory operations, not for this trip's prefetch
     if constexpr (C > 0) {
-      // packed bf16 pairs straight into v_dot2_f32_bf16: weight word w holds
-      // elements (e, 2c), (e, 2c+1), camera word c holds cam[2c], cam[2c+1];
-      // the products are exact in fp32 and accumulate in c order
-      const uint32_t* cr[2] = {camw + (s - s_begin) * CW, camw + (s1 - s_begin) * CW};
 #pragma unroll
-      for (int e = 0; e < kCPT; ++e) {
-        float acc[2] = {0.f, 0.f};
+      for (int t = 0; t < kTrip; ++t) {
+        const int r = sv[t] - s_begin;
+        if (cam_new[r]) {   // workgroup-uniform
+          // packed bf16 pairs straight into v_dot2_f32_bf16: weight word w
+          // holds elements (e, 2c), (e, 2c+1), camera word c holds cam[2c],
+          // cam[2c+1]; the products are exact in fp32 and accumulate in c order
+          const u32x4* wr = reinterpret_cast<const u32x4*>(
+              (is_k ? a.w_cam_k : a.w_cam_q) + (int64_t)c0 * C);
+          const uint32_t* cr = camw + r * CW;
+          u32x4 wv[kCPT * CW / 4];
 #pragma unroll
-        for (int c = 0; c < CW; ++c) {
-          const int w = e * CW + c;
-          // (through a scalar temporary: a bit-cast applied to a vector
-          // element subscript directly reads element 0)
-          const uint32_t uw = wc[w >> 2][w & 3];
-          const bf16x2 xw = __builtin_bit_cast(bf16x2, uw);
+          for (int i = 0; i < kCPT * CW / 4; ++i) wv[i] = wr[i];
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const uint32_t uc = cr[t][c];
-            acc[t] = __builtin_amdgcn_fdot2_f32_bf16(xw, __builtin_bit_cast(bf16x2, uc), acc[t],
-                                                     false);
+          for (int e = 0; e < kCPT; ++e) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < CW; ++c) {
+              const int w = e * CW + c;
+              // (through a scalar temporary: a bit-cast applied to a vector
+              // element subscript directly reads element 0)
+              const uint32_t uw = wv[w >> 2][w & 3];
+              acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, uw),
+                                                    __builtin_bit_cast(bf16x2, cr[c]), acc, false);
+            }
+            camp[e] = acc;
           }
+#pragma unroll
+          for (int e = 0; e < kCPT; e += 2) rbf2(camp[e], camp[e + 1]);
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) q[t][e] = rbf(q[t][e] + rbf(acc[t]));
+        for (int e = 0; e < kCPT; ++e) cpt[t][e] = camp[e];
       }
     }
-    float ss[2] = {0.f, 0.f};
+    // unconditional (clamped to the last token past the end), so that the
+    // compiler knows exactly which loads are in flight at the first use of `use`
+    fetch(nxt, s + kTrip);
+    float q[kTrip][kCPT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < kTrip; ++t)
+#pragma unroll
+      for (int e = 0; e < kCPT / 2; ++e) {
+        q[t][2 * e] = __uint_as_float(use.x[t][e] << 16);
+        q[t][2 * e + 1] = __uint_as_float(use.x[t][e] & 0xffff0000u);
+      }
+    if constexpr (C > 0) {
+#pragma unroll
+      for (int t = 0; t < kTrip; ++t)
+#pragma unroll
+        for (int e = 0; e < kCPT; e += 2) {
+          q[t][e] += cpt[t][e];
+          q[t][e + 1] += cpt[t][e + 1];
+          rbf2(q[t][e], q[t][e + 1]);
+        }
+    }
+    float ss[kTrip];
+#pragma unroll
+    for (int t = 0; t < kTrip; ++t) {
+      ss[t] = 0.f;
 #pragma unroll
       for (int e = 0; e < kCPT; ++e) ss[t] = fmaf(q[t][e], q[t][e], ss[t]);
-    block_sum<2>(ss, red);
+    }
+    block_sum<kTrip>(ss, red, parity);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (t == 1 && !second) break;
-      const float inv = rsqrtf(ss[t] / (float)dim + a.eps);
+    for (int t = 0; t < kTrip; ++t) {
+      const float inv = __builtin_amdgcn_rsqf(ss[t] * inv_dim + a.eps);
 #pragma unroll
-      for (int e = 0; e < kCPT; ++e) q[t][e] = rbf(rbf(q[t][e] * inv) * g[e]);
+      for (int e = 0; e < kCPT; e += 2) {
+        q[t][e] *= inv;
+        q[t][e + 1] *= inv;
+        rbf2(q[t][e], q[t][e + 1]);
+        q[t][e] *= g[e];
+        q[t][e + 1] *= g[e + 1];
+        rbf2(q[t][e], q[t][e + 1]);
+      }
       // RoPE on (even, odd) channel pairs of this head
       chw_t qv;
 #pragma unroll
       for (int e = 0; e < kCPT / 2; ++e) {
-        const float c = cs[t][e], sv = sn[t][e];
-        const float qr = q[t][2 * e] * c - q[t][2 * e + 1] * sv;
-        const float qi = q[t][2 * e] * sv + q[t][2 * e + 1] * c;
+        const float qr = q[t][2 * e] * use.c[t][e] - q[t][2 * e + 1] * use.s[t][e];
+        const float qi = q[t][2 * e] * use.s[t][e] + q[t][2 * e + 1] * use.c[t][e];
         qv[e] = f2bf(qr) | (f2bf(qi) << 16);
       }
-      const int64_t off = (int64_t)(s + t) * a.out_stride_s + (int64_t)head * a.out_stride_h + d0;
+      const int64_t off = (int64_t)sv[t] * a.out_stride_s + (int64_t)head * a.out_stride_h + d0;
       *reinterpret_cast<chw_t*>(out + off) = qv;
-      if (copy_v) *reinterpret_cast<chw_t*>(a.v_out + off) = v4[t];
+      if (copy_v)
+        *reinterpret_cast<chw_t*>(a.v_out + off) =
+            *reinterpret_cast<const chw_t*>(a.vx + (uint32_t)(sv[t] * dim + c0));
     }
+  };
+  // two trips per iteration, the register sets and the reduction buffers
+  // alternating
+  Pf pa, pb;
+  fetch(pa, s_begin);
+  for (int s = s_begin; s < s_end; s += 2 * kTrip) {
+    trip(s, 0, pa, pb);
+    if (s + kTrip < s_end) trip(s + kTrip, 1, pb, pa);
   }
 }
 
@@ -224,16 +342,30 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   HIER_REQUIRE(((uintptr_t)a.rope_cos & 15u) == 0 && ((uintptr_t)a.rope_sin & 15u) == 0 &&
                    (!cam || ((uintptr_t)a.cam & 7u) == 0),
                HIER_EINVAL, "RoPE tables must be 16-byte and camera rows 8-byte aligned");
+  HIER_REQUIRE((int64_t)a.S * dim <= INT32_MAX, HIER_EUNSUPPORTED,
+               "S x model dim must stay below 2^31 elements (got %d x %d)", a.S, dim);
   if (a.S == 0) return HIER_OK;
   const int grid = (a.S + kTokens - 1) / kTokens;
   const int threads = nthr;
   const hipStream_t st = (hipStream_t)stream;
+  const dim3 g2(grid, 2);
+  const bool v = a.v_out != nullptr;
   if (kCPT == 4) {
-    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 4>), dim3(grid, 2), dim3(threads), 0, st, a);
-    else hipLaunchKernelGGL((prologue_kernel<0, 4>), dim3(grid, 2), dim3(threads), 0, st, a);
+    if (cam) {
+      if (v) hipLaunchKernelGGL((prologue_kernel<12, 4, true>), g2, dim3(threads), 0, st, a);
+      else hipLaunchKernelGGL((prologue_kernel<12, 4, false>), g2, dim3(threads), 0, st, a);
+    } else {
+      if (v) hipLaunchKernelGGL((prologue_kernel<0, 4, true>), g2, dim3(threads), 0, st, a);
+      else hipLaunchKernelGGL((prologue_kernel<0, 4, false>), g2, dim3(threads), 0, st, a);
+    }
   } else {
-    if (cam) hipLaunchKernelGGL((prologue_kernel<12, 8>), dim3(grid, 2), dim3(threads), 0, st, a);
-    else hipLaunchKernelGGL((prologue_kernel<0, 8>), dim3(grid, 2), dim3(threads), 0, st, a);
+    if (cam) {
+      if (v) hipLaunchKernelGGL((prologue_kernel<12, 8, true>), g2, dim3(threads), 0, st, a);
+      else hipLaunchKernelGGL((prologue_kernel<12, 8, false>), g2, dim3(threads), 0, st, a);
+    } else {
+      if (v) hipLaunchKernelGGL((prologue_kernel<0, 8, true>), g2, dim3(threads), 0, st, a);
+      else hipLaunchKernelGGL((prologue_kernel<0, 8, false>), g2, dim3(threads), 0, st, a);
+    }
   }
   return hier::check_launch("prologue_kernel");
 }

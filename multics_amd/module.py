@@ -158,18 +158,20 @@ class SelfAttention(nn.Module):
                 and self.head_dim in (64, 128))
 
     def _project_fused(self, x, freqs, cam_tokens=None):
-        """No-grad Q/K/V: GEMMs, then the fused HIP prologue.  Returns [S, H, D]
-        views of head-major storage (each head's rows one contiguous slab, the
-        layout the attention kernel gathers keys from fastest)."""
+        """No-grad Q/K/V: GEMMs, then the fused HIP prologue on q and k.
+        Returns token-major [S, H, D] tensors; V is the v projection itself,
+        read in place (the attention kernels take any row / head strides and
+        run at the same speed on token-major and head-major K/V)."""
         cam = self._check_cam(x, cam_tokens)
         qx, kx, vx = (lin(x)[0].contiguous() for lin in (self.q, self.k, self.v))
         cs, sn = freqs_to_cos_sin(freqs, device=x.device)
-        return qkv_prologue(
-            qx, kx, vx, norm_q_w=self.norm_q.weight, norm_k_w=self.norm_k.weight, rope_cos=cs,
+        q, k, _ = qkv_prologue(
+            qx, kx, None, norm_q_w=self.norm_q.weight, norm_k_w=self.norm_k.weight, rope_cos=cs,
             rope_sin=sn, num_heads=self.num_heads, eps=self.norm_q.eps,
             cam=None if cam is None else cam[0],
             w_cam_q=None if cam is None else self.cam_q.weight,
-            w_cam_k=None if cam is None else self.cam_k.weight, out_layout="hsd")
+            w_cam_k=None if cam is None else self.cam_k.weight, out_layout="shd")
+        return q, k, vx.view(vx.shape[0], self.num_heads, self.head_dim)
 
     def _qkv_blocks(self, x, freqs, cam_tokens):
         """[S, H, D] bf16 Q/K/V of a [1, S, dim] input (fused prologue when it applies)."""

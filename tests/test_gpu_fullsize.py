@@ -102,12 +102,12 @@ def test_forward_full_size_sampled_rows(cfg):
 
 def test_forward_c2_as_benchmarked():
     """The headline configuration exactly as ``bench.py`` times it: C2 with
-    all 24 heads, Q/K/V stored head-major (``[H, S, D]`` presented as
-    ``[S, H, D]`` views, the layout ``qkv_prologue(out_layout="hsd")`` and
-    the module's no-grad path write).  Sampled rows against the oracle at the
-    north-star bounds; the whole output bit-identical to the same forward on
-    token-major ``[S, H, D]`` copies of the inputs (the layout changes only the
-    addresses the kernel reads)."""
+    all 24 heads, Q/K/V token-major ``[S, H, D]`` (the layout of the module's
+    no-grad path: prologue q / k, the v projection in place).  Sampled rows
+    against the oracle at the north-star bounds; the whole output bit-identical
+    to the same forward on head-major storage (``[H, S, D]`` presented as
+    ``[S, H, D]`` views: the layout changes only the addresses the kernel
+    reads)."""
     need_gpu()
     meta, topo, D = _case("c2")
     H = bench.CONFIGS["c2"][8]
