@@ -549,9 +549,11 @@ def main():
 
     g = torch.Generator(device=dev).manual_seed(SEED)
     mk = lambda: (torch.randn(H, S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
-    # token-major [S, H, D], the layout the module's no-grad path feeds the
-    # kernel (prologue q / k, the v projection in place)
-    q, k, v = (mk().permute(1, 0, 2).contiguous() for _ in range(3))
+    # the layout the module's no-grad path feeds the kernel: q / k head-major
+    # (the prologue's [H, S, D] storage as [S, H, D] views), v token-major
+    # (the v projection, read in place)
+    q, k = (mk().permute(1, 0, 2) for _ in range(2))
+    v = mk().permute(1, 0, 2).contiguous()
     out = torch.empty(S, H, D, dtype=torch.bfloat16, device=dev)
 
     def step():
@@ -575,7 +577,7 @@ def main():
     cs, sn = rope_tables(P, T, L, N * KL + KG, D, dev)
     pro = time_events(lambda: qkv_prologue(qx, kx, None, norm_q_w=nw, norm_k_w=nw, rope_cos=cs,
                                            rope_sin=sn, num_heads=H, eps=1e-6, cam=cam,
-                                           w_cam_q=wcq, w_cam_k=wck, out_layout="shd"),
+                                           w_cam_q=wcq, w_cam_k=wck, out_layout="hsd"),
                       max(args.steps // 5, 3), 2)
     pro_ms = float(np.median(pro))
 

@@ -159,9 +159,10 @@ class SelfAttention(nn.Module):
 
     def _project_fused(self, x, freqs, cam_tokens=None):
         """No-grad Q/K/V: GEMMs, then the fused HIP prologue on q and k.
-        Returns token-major [S, H, D] tensors; V is the v projection itself,
-        read in place (the attention kernels take any row / head strides and
-        run at the same speed on token-major and head-major K/V)."""
+        Returns [S, H, D] views: q and k of head-major storage (each head's
+        keys one contiguous slab: the K gathers fetch fewer bytes from HBM,
+        at the same speed), V the v projection itself, read in place (the
+        attention kernels take any row / head strides)."""
         cam = self._check_cam(x, cam_tokens)
         qx, kx, vx = (lin(x)[0].contiguous() for lin in (self.q, self.k, self.v))
         cs, sn = freqs_to_cos_sin(freqs, device=x.device)
@@ -170,7 +171,7 @@ class SelfAttention(nn.Module):
             rope_sin=sn, num_heads=self.num_heads, eps=self.norm_q.eps,
             cam=None if cam is None else cam[0],
             w_cam_q=None if cam is None else self.cam_q.weight,
-            w_cam_k=None if cam is None else self.cam_k.weight, out_layout="shd")
+            w_cam_k=None if cam is None else self.cam_k.weight, out_layout="hsd")
         return q, k, vx.view(vx.shape[0], self.num_heads, self.head_dim)
 
     def _qkv_blocks(self, x, freqs, cam_tokens):

@@ -102,12 +102,12 @@ def test_forward_full_size_sampled_rows(cfg):
 
 def test_forward_c2_as_benchmarked():
     """The headline configuration exactly as ``bench.py`` times it: C2 with
-    all 24 heads, Q/K/V token-major ``[S, H, D]`` (the layout of the module's
-    no-grad path: prologue q / k, the v projection in place).  Sampled rows
-    against the oracle at the north-star bounds; the whole output bit-identical
-    to the same forward on head-major storage (``[H, S, D]`` presented as
-    ``[S, H, D]`` views: the layout changes only the addresses the kernel
-    reads)."""
+    all 24 heads, Q/K head-major (``[H, S, D]`` storage presented as
+    ``[S, H, D]`` views, as the prologue writes them on the module's no-grad
+    path) and V token-major (the v projection read in place).  Sampled rows
+    against the oracle at the north-star bounds; the whole output
+    bit-identical to the same forward on token-major copies of all three (the
+    layout changes only the addresses the kernel reads)."""
     need_gpu()
     meta, topo, D = _case("c2")
     H = bench.CONFIGS["c2"][8]
@@ -117,12 +117,13 @@ def test_forward_c2_as_benchmarked():
     g = torch.Generator().manual_seed(31)
     qh, kh, vh = ((torch.randn(H, topo.S, D, generator=g) * 0.5).to(torch.bfloat16)
                   for _ in range(3))
-    qd, kd, vd = (t.cuda().permute(1, 0, 2) for t in (qh, kh, vh))
-    assert qd.stride() == (D, topo.S * D, 1)
+    qd, kd = (t.cuda().permute(1, 0, 2) for t in (qh, kh))
+    vd = vh.cuda().permute(1, 0, 2).contiguous()
+    assert qd.stride() == (D, topo.S * D, 1) and vd.stride() == (H * D, D, 1)
     out = torch.zeros(topo.S, H, D, dtype=torch.bfloat16, device="cuda")
     hier_attention_forward(qd, kd, vd, tiles, out)
     torch.cuda.synchronize()
-    say("  head-major done; token-major copies")
+    say("  benchmarked layout done; token-major copies")
     out_shd = torch.zeros_like(out)
     hier_attention_forward(qd.contiguous(), kd.contiguous(), vd.contiguous(), tiles, out_shd)
     torch.cuda.synchronize()
