@@ -12,18 +12,25 @@
 // with the same bf16 rounding points as the reference.  The reference rotates
 // in float64; here the rotation runs in fp32 from fp32 cos/sin tables, so a
 // result can differ from the reference by one bf16 ulp.  The RMS spans all
-// heads (the full model dim), so one workgroup owns whole tokens of one
-// projection (q or k): dim/CPT threads x CPT channels (CPT = 4 up to dim 3072,
-// else 8).  The workgroup walks kTokens tokens two at a time: one workgroup
-// reduction (DPP and lane swaps inside each wave, one LDS barrier across
-// waves) serves both tokens, and the next two tokens' projections and RoPE
-// rows are loaded into a second register set while the current two are
-// computed.  A token's camera row is the same for every token of a player's
-// frame (zero for hub tokens), so the camera product (v_dot2_f32_bf16 over
-// packed bf16 pairs, weights read when needed) is recomputed only where the
-// row changes.  With v_out the q workgroups also copy V into the requested
-// layout.
+// heads (the full model dim), so each token of a projection (q or k) is owned
+// whole by one wave or one workgroup:
+//   * model dims that are multiples of 512 (up to 4096): row_prologue_kernel,
+//     one wave per run of consecutive tokens, 8*NCH channels per lane, the RMS
+//     a register sum plus one DPP wave reduction (no LDS traffic, no barrier
+//     per token);
+//   * other dims: prologue_kernel, one workgroup of dim/CPT threads x CPT
+//     channels (CPT = 4 up to dim 3072, else 8) walking kTokens tokens two at
+//     a time, one workgroup reduction (DPP and lane swaps inside each wave,
+//     one LDS barrier across waves) per two tokens.
+// Both load the next token's projection and RoPE rows into a second register
+// set while the current one is computed.  A token's camera row is the same
+// for every token of a player's frame (zero for hub tokens), so the camera
+// product (v_dot2_f32_bf16 over packed bf16 pairs, weights read when needed)
+// is recomputed only where the row changes.  With v_out the q waves /
+// workgroups also copy V into the requested layout.
 #include "hier_common.h"
+
+#include <algorithm>
 
 namespace {
 
@@ -46,6 +53,19 @@ __device__ __forceinline__ void rbf2(float& a, float& b) {
   const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
   a = __uint_as_float(u << 16);
   b = __uint_as_float(u & 0xffff0000u);
+}
+
+// One value rounded to bf16 and back in one instruction: converting the pair
+// (0, x) puts bf16(x) in the high half over a zero low half, which is the
+// rounded value as an fp32.
+__device__ __forceinline__ float rbf1(float x) {
+  const f32x2 v = {0.f, x};
+  return __uint_as_float(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2)));
+}
+// A pair of floats as packed bf16 (round to nearest even), one conversion.
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Sum over the 64 lanes of a wave, left in every lane: DPP within rows of
@@ -314,6 +334,188 @@ __global__ __launch_bounds__(kCPT == 4 ? 768 : 512) void prologue_kernel(HierPro
   }
 }
 
+// ---- one wave per token (model dims that are multiples of 512) --------------
+//
+// A wave owns a run of consecutive tokens of one projection and walks it one
+// token at a time; lane l holds the NCH 8-channel chunks 8*(64j + l) of the
+// token (each chunk of the wave is 1 KB contiguous), so the RMS is one
+// register sum and one DPP wave reduction: no LDS and no barrier.  The 8
+// channels of a chunk are 4 RoPE pairs of one head, at the same pair index
+// 4*(l mod D/8) for every chunk, so a token's cos / sin come in one 16-byte
+// load each.  The next token's projection, RoPE rows (and V) are loaded into
+// the other of two register sets while the current token is computed.
+
+template <int NCH, bool kCopyV>
+struct RowPf {
+  u32x4 x[NCH];
+  u32x4 v[kCopyV ? NCH : 1];
+  float4 c, s;
+};
+
+template <int NCH, int C, bool kCopyV>
+__global__ __launch_bounds__(256, NCH <= 6 && !kCopyV ? 3 : 2) void row_prologue_kernel(HierPrologueArgs a,
+                                                                                     int tpw) {
+  constexpr int CW = C > 0 ? C / 2 : 1;      // packed camera words per token
+  constexpr int dim = NCH * 512;
+  const int lane = threadIdx.x & 63;
+  const bool is_k = blockIdx.y != 0;
+  const bool copy_v = kCopyV && !is_k;
+  const int s_begin = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))) * tpw;
+  // RMSNorm gains as fp32, [chunk][half][lane] float4s (conflict-free reads),
+  // shared by the workgroup's waves (all of one projection)
+  __shared__ float4 g_lds[NCH * 2 * 64];
+  for (int i = threadIdx.x; i < NCH * 64; i += blockDim.x) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>((is_k ? a.norm_k_w : a.norm_q_w) + 8 * i);
+    const int j = i >> 6, l = i & 63;
+    g_lds[(2 * j) * 64 + l] = make_float4(__uint_as_float(w[0] << 16), __uint_as_float(w[0] & 0xffff0000u),
+                                          __uint_as_float(w[1] << 16), __uint_as_float(w[1] & 0xffff0000u));
+    g_lds[(2 * j + 1) * 64 + l] = make_float4(__uint_as_float(w[2] << 16), __uint_as_float(w[2] & 0xffff0000u),
+                                              __uint_as_float(w[3] << 16), __uint_as_float(w[3] & 0xffff0000u));
+  }
+  __syncthreads();
+  if (s_begin >= a.S) return;   // wave-uniform; no barrier follows
+  const int s_end = min(a.S, s_begin + tpw);
+  const uint16_t* const xin = is_k ? a.kx : a.qx;
+  uint16_t* const out = is_k ? a.k_out : a.q_out;
+  const int D = a.D, half = D / 2;
+  const int d0 = (8 * lane) % D;             // the same in every chunk (D divides 512)
+  const int m0 = d0 / 2;
+  const float inv_dim = 1.f / (float)dim;
+  // output offset of chunk j, token term aside (every output offset is below
+  // S * dim < 2^31, checked by the launcher)
+  auto ooff = [&](int j) {
+    return (uint32_t)((8 * (64 * j + lane)) / D) * (uint32_t)a.out_stride_h + (uint32_t)d0;
+  };
+  // element offsets of the [S, dim] projections fit in 32 bits (checked by the launcher)
+  auto fetch = [&](RowPf<NCH, kCopyV>& f, int s) {
+    const int st = min(s, s_end - 1);
+    const uint32_t r0 = (uint32_t)(st * dim + 8 * lane);
+    const u32x4* xr = reinterpret_cast<const u32x4*>(xin + r0);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) f.x[j] = xr[64 * j];
+    if (copy_v) {
+      const u32x4* vr = reinterpret_cast<const u32x4*>(a.vx + r0);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) f.v[j] = vr[64 * j];
+    }
+    f.c = *reinterpret_cast<const float4*>(a.rope_cos + (uint32_t)(st * half + m0));
+    f.s = *reinterpret_cast<const float4*>(a.rope_sin + (uint32_t)(st * half + m0));
+  };
+  // camera product of the last camera row seen, bf16-rounded, packed pairs;
+  // a token's row is the same for every token of a player's frame (zero for
+  // hub tokens), so it is recomputed only where the row changes
+  // (in this wave's LDS slot: each lane reads back only what it wrote)
+  __shared__ u32x4 camp_lds[C > 0 ? 4 * NCH * 64 : 1];
+  u32x4* const camp = camp_lds + (C > 0 ? (s_begin / tpw % 4) * NCH * 64 + lane : 0);
+  uint32_t camw_prev[CW] = {};
+  auto camera = [&](int s) {
+    if constexpr (C > 0) {
+      const uint32_t* cr = reinterpret_cast<const uint32_t*>(a.cam + (int64_t)s * C);
+      uint32_t cw[CW];
+      bool diff = s == s_begin;
+#pragma unroll
+      for (int c = 0; c < CW; ++c) {
+        cw[c] = cr[c];
+        diff = diff || cw[c] != camw_prev[c];
+      }
+      if (diff) {   // wave-uniform
+#pragma unroll
+        for (int c = 0; c < CW; ++c) camw_prev[c] = cw[c];
+        const uint16_t* wbase = is_k ? a.w_cam_k : a.w_cam_q;
+        // the weight addresses are formed here, not hoisted out of the token
+        // loop (where they would hold 2*NCH registers for a rare branch)
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+          // weight word e*CW + c holds W[cj + e][2c], W[cj + e][2c + 1]; the
+          // products are exact in fp32 and accumulate in c order
+          const u32x4* wr = reinterpret_cast<const u32x4*>(wbase) + (uint32_t)(64 * j + ln) * (uint32_t)C;
+          float pr[8];
+#pragma unroll
+          for (int hlf = 0; hlf < 2; ++hlf) {   // four channels' weights in registers at a time
+            u32x4 wv[CW];
+#pragma unroll
+            for (int i = 0; i < CW; ++i) wv[i] = wr[hlf * CW + i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float acc = 0.f;
+#pragma unroll
+              for (int c = 0; c < CW; ++c) {
+                const int w = e * CW + c;
+                const uint32_t uw = wv[w >> 2][w & 3];
+                acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, uw),
+                                                      __builtin_bit_cast(bf16x2, cw[c]), acc, false);
+              }
+              pr[4 * hlf + e] = acc;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          u32x4 cp;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cp[e] = f2bf(pr[2 * e]) | (f2bf(pr[2 * e + 1]) << 16);
+          camp[64 * j] = cp;
+        }
+      }
+    }
+  };
+  auto token = [&](int s, const RowPf<NCH, kCopyV>& use, RowPf<NCH, kCopyV>& nxt) {
+    camera(s);
+    // unconditional (clamped to the last token past the end), so that the
+    // compiler knows exactly which loads are in flight at the first use of `use`
+    fetch(nxt, s + 1);
+    // the projection plus the camera product, rounded to bf16 (packed pairs)
+    u32x4 qp[NCH];
+    float ssp[4] = {0.f, 0.f, 0.f, 0.f};   // sum of squares, four independent chains
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      u32x4 cp;
+      if constexpr (C > 0) cp = camp[64 * j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t u = use.x[j][e];
+        if constexpr (C > 0)
+          u = pack_bf2(__uint_as_float(u << 16) + __uint_as_float(cp[e] << 16),
+                       __uint_as_float(u & 0xffff0000u) + __uint_as_float(cp[e] & 0xffff0000u));
+        qp[j][e] = u;
+        // bf16 squares are exact in fp32
+        ssp[e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u),
+                                                 __builtin_bit_cast(bf16x2, u), ssp[e], false);
+      }
+    }
+    const float ss = wave_sum((ssp[0] + ssp[1]) + (ssp[2] + ssp[3]));
+    // unpacked again below rather than kept unpacked (half the registers)
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) asm volatile("" : "+v"(qp[j]));
+    const float inv = __builtin_amdgcn_rsqf(ss * inv_dim + a.eps);
+    const float cs[4] = {use.c.x, use.c.y, use.c.z, use.c.w};
+    const float sn[4] = {use.s.x, use.s.y, use.s.z, use.s.w};
+    const uint32_t srow = (uint32_t)s * (uint32_t)a.out_stride_s;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const float4 ga = g_lds[(2 * j) * 64 + lane], gb = g_lds[(2 * j + 1) * 64 + lane];
+      const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = rbf1(rbf1(__uint_as_float(qp[j][e] << 16) * inv) * gv[2 * e]);
+        const float x1 = rbf1(rbf1(__uint_as_float(qp[j][e] & 0xffff0000u) * inv) * gv[2 * e + 1]);
+        // RoPE on the (even, odd) pair
+        o[e] = pack_bf2(x0 * cs[e] - x1 * sn[e], x0 * sn[e] + x1 * cs[e]);
+      }
+      const uint32_t off = srow + ooff(j);
+      *reinterpret_cast<u32x4*>(out + off) = o;
+      if (copy_v) *reinterpret_cast<u32x4*>(a.v_out + off) = use.v[j];
+    }
+  };
+  RowPf<NCH, kCopyV> pa, pb;
+  fetch(pa, s_begin);
+  for (int s = s_begin; s < s_end; s += 2) {
+    token(s, pa, pb);
+    if (s + 1 < s_end) token(s + 1, pb, pa);
+  }
+}
+
 }  // namespace
 
 extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
@@ -345,11 +547,37 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   HIER_REQUIRE((int64_t)a.S * dim <= INT32_MAX, HIER_EUNSUPPORTED,
                "S x model dim must stay below 2^31 elements (got %d x %d)", a.S, dim);
   if (a.S == 0) return HIER_OK;
+  const hipStream_t st = (hipStream_t)stream;
+  const bool v = a.v_out != nullptr;
+  const int nch = dim / 512;
+  if (dim % 512 == 0 && (nch <= 4 || nch == 6 || nch == 8) && a.out_stride_s % 8 == 0 &&
+      a.out_stride_h % 8 == 0 && (!cam || (((uintptr_t)a.w_cam_q | (uintptr_t)a.w_cam_k) & 15u) == 0)) {
+    // one wave per run of tpw tokens, about sixteen waves per CU over both projections
+    const int tpw = std::max(4, (int)((2ll * a.S + 4095) / 4096));
+    const int waves = (a.S + tpw - 1) / tpw;
+    const dim3 g2((waves + 3) / 4, 2);
+#define HIER_ROW_LAUNCH(N)                                                                        \
+  if (nch == N) {                                                                                 \
+    if (cam) {                                                                                    \
+      if (v) hipLaunchKernelGGL((row_prologue_kernel<N, 12, true>), g2, dim3(256), 0, st, a, tpw);  \
+      else hipLaunchKernelGGL((row_prologue_kernel<N, 12, false>), g2, dim3(256), 0, st, a, tpw);   \
+    } else {                                                                                      \
+      if (v) hipLaunchKernelGGL((row_prologue_kernel<N, 0, true>), g2, dim3(256), 0, st, a, tpw);   \
+      else hipLaunchKernelGGL((row_prologue_kernel<N, 0, false>), g2, dim3(256), 0, st, a, tpw);    \
+    }                                                                                             \
+  }
+    HIER_ROW_LAUNCH(1)
+    HIER_ROW_LAUNCH(2)
+    HIER_ROW_LAUNCH(3)
+    HIER_ROW_LAUNCH(4)
+    HIER_ROW_LAUNCH(6)
+    HIER_ROW_LAUNCH(8)
+#undef HIER_ROW_LAUNCH
+    return hier::check_launch("row_prologue_kernel");
+  }
   const int grid = (a.S + kTokens - 1) / kTokens;
   const int threads = nthr;
-  const hipStream_t st = (hipStream_t)stream;
   const dim3 g2(grid, 2);
-  const bool v = a.v_out != nullptr;
   if (kCPT == 4) {
     if (cam) {
       if (v) hipLaunchKernelGGL((prologue_kernel<12, 4, true>), g2, dim3(threads), 0, st, a);

@@ -20,11 +20,14 @@ def _freqs(P, T, h, w, KG_total):
 
 @pytest.mark.parametrize("camera", [False, True])
 @pytest.mark.parametrize("layout", ["shd", "hsd"])
-@pytest.mark.parametrize("shape", ["small", "odd_tokens", "dim4096"])
+@pytest.mark.parametrize("shape", ["small", "odd_tokens", "dim4096", "dim3072", "dim768"])
 def test_prologue_matches_oracle(camera, layout, shape):
-    """small: 168 tokens, dim 512 (4 channels per thread); odd_tokens: 141
-    tokens, so the last workgroup ends on a token paired with itself;
-    dim4096: 32 heads, 8 channels per thread."""
+    """Model dims that are multiples of 512 run one wave per token run
+    (row_prologue_kernel), others the workgroup-per-token kernel.  small: 168
+    tokens, dim 512; odd_tokens: 141 tokens, so a wave's run ends on a token
+    paired with itself; dim4096: 32 heads (eight chunks per lane); dim3072:
+    the C2 model dim (six chunks), with camera rows changing inside a wave's
+    run; dim768: 6 heads, the workgroup kernel."""
     need_gpu()
     say("prologue camera", camera, layout, shape)
     P, T, h, w, H, D = 2, 3, 4, 5, 4, 128
@@ -33,6 +36,10 @@ def test_prologue_matches_oracle(camera, layout, shape):
         h, w, K_total = 3, 5, 2 * 5 + 7
     elif shape == "dim4096":
         T, H = 2, 32
+    elif shape == "dim3072":
+        T, H = 2, 24
+    elif shape == "dim768":
+        H = 6
     S = P * T * h * w + T * K_total
     assert shape != "odd_tokens" or S % 2 == 1
     dim = H * D
