@@ -20,17 +20,20 @@ def _freqs(P, T, h, w, KG_total):
 
 @pytest.mark.parametrize("camera", [False, True])
 @pytest.mark.parametrize("layout", ["shd", "hsd"])
-@pytest.mark.parametrize("shape", ["small", "odd_tokens", "dim4096", "dim3072", "dim768"])
+@pytest.mark.parametrize("shape", ["small", "odd_tokens", "dim4096", "dim3072", "dim768", "d64"])
 def test_prologue_matches_oracle(camera, layout, shape):
     """Model dims that are multiples of 512 run one wave per token run
     (row_prologue_kernel), others the workgroup-per-token kernel.  small: 168
     tokens, dim 512; odd_tokens: 141 tokens, so a wave's run ends on a token
     paired with itself; dim4096: 32 heads (eight chunks per lane); dim3072:
     the C2 model dim (six chunks), with camera rows changing inside a wave's
-    run; dim768: 6 heads, the workgroup kernel."""
+    run; dim768: 6 heads, the workgroup kernel; d64: head dim 64, 8 heads
+    (dim 512, the wave kernel's D = 64 pair indexing)."""
     need_gpu()
     say("prologue camera", camera, layout, shape)
     P, T, h, w, H, D = 2, 3, 4, 5, 4, 128
+    if shape == "d64":
+        H, D = 8, 64
     K_total = 2 * 5 + 6
     if shape == "odd_tokens":
         h, w, K_total = 3, 5, 2 * 5 + 7
@@ -50,6 +53,8 @@ def test_prologue_matches_oracle(camera, layout, shape):
     wq = (1 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16)
     wk = (1 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16)
     freqs = _freqs(P, T, h, w, K_total)
+    if D == 64:
+        freqs = freqs[..., :32].contiguous()   # any unit rotations serve the comparison
     cam = wcq = wck = None
     if camera:
         cam = torch.zeros(S, 12)
