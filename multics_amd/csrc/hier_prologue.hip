@@ -381,8 +381,8 @@ __global__ __launch_bounds__(256, NCH <= 6 && !kCopyV ? 3 : 2) void row_prologue
   const int d0 = (8 * lane) % D;             // the same in every chunk (D divides 512)
   const int m0 = d0 / 2;
   const float inv_dim = 1.f / (float)dim;
-  // output offset of chunk j, token term aside (every output offset is below
-  // S * dim < 2^31, checked by the launcher)
+  // output offset of chunk j, token term aside (the launcher runs this kernel
+  // only when every output offset fits in 31 bits)
   auto ooff = [&](int j) {
     return (uint32_t)((8 * (64 * j + lane)) / D) * (uint32_t)a.out_stride_h + (uint32_t)d0;
   };
@@ -550,8 +550,11 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   const hipStream_t st = (hipStream_t)stream;
   const bool v = a.v_out != nullptr;
   const int nch = dim / 512;
+  // the wave kernel forms output offsets in 32 bits
+  const int64_t out_ext = (int64_t)(a.S - 1) * a.out_stride_s + (int64_t)(a.H - 1) * a.out_stride_h + a.D;
   if (dim % 512 == 0 && (nch <= 4 || nch == 6 || nch == 8) && a.out_stride_s % 8 == 0 &&
-      a.out_stride_h % 8 == 0 && (!cam || (((uintptr_t)a.w_cam_q | (uintptr_t)a.w_cam_k) & 15u) == 0)) {
+      a.out_stride_h % 8 == 0 && a.out_stride_s >= 0 && a.out_stride_h >= 0 && out_ext <= INT32_MAX &&
+      (!cam || (((uintptr_t)a.w_cam_q | (uintptr_t)a.w_cam_k) & 15u) == 0)) {
     // one wave per run of tpw tokens, about sixteen waves per CU over both projections
     const int tpw = std::max(4, (int)((2ll * a.S + 4095) / 4096));
     const int waves = (a.S + tpw - 1) / tpw;
