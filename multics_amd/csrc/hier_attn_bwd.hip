@@ -3,7 +3,7 @@
 // With P = exp(scale * Q K^T - lse) (lse from the forward), dP = dO V^T,
 // delta = rowsum(dO * O) and dS = P * (dP - delta):
 //   dQ = scale * dS K,   dK = scale * dS^T Q,   dV = P^T dO.
-// Three kernels, each writing every gradient row from exactly one workgroup
+// Two kernels, each writing every gradient row from exactly one workgroup
 // (deterministic, no atomics):
 //
 // dq_kernel   query-major, over the forward tile list (128 query rows per
@@ -13,18 +13,16 @@
 //               dS^T = P^T (dP^T - delta)
 //               dQ^T += K^T dS^T      (K transposed out of LDS)
 //             Also writes delta and lse2 = lse * log2(e) per query row.
-// dv_kernel / dk_kernel
-//             key-major, over the transposed tile list (128 key rows per
-//             item, lists of query rows with a bitmask over key frames), one
-//             kernel per gradient so that each runs two waves per SIMD (one
-//             wave owning both the dK and the dV accumulators needs more than
-//             the 256 registers of two waves, and one wave per SIMD is
-//             VALU-issue bound here).  Per 32-query block:
-//               dv_kernel (software-pipelined like the forward):
-//                        S = Q K^T, P;  dV^T += dO^T P
-//               dk_kernel: S = Q K^T, dP = dO V^T, dS;  dK^T += Q^T dS
+// dkv_kernel  key-major, over the transposed tile list (128 key rows per
+//             item, lists of query rows with a bitmask over key frames),
+//             eight waves: wave w and wave w+4 own the same 32 key rows (one
+//             wave cannot hold both accumulators at two waves per SIMD).
+//             Per 64-query tile:
+//               wave w:   S = Q K^T, P;  P to LDS;  dV^T += dO^T P
+//               wave w+4: dP = dO V^T;  dS = P (dP - delta);  dK^T += Q^T dS
 //             (Q / dO rows from LDS, K^T / V^T in registers, Q / dO
-//             transposed out of LDS for the accumulation).
+//             transposed out of LDS for the accumulations), with the S / dP
+//             products of tile t+1 overlapping the accumulations of tile t.
 // The lane layouts are the forward's: an MFMA result keeps one column per
 // lane and its rows {8*(r/4) + 4*(lane/32) + r%4}, which is exactly the
 // permuted k order of the next MFMA's register operand, so P and dS go from
@@ -35,6 +33,7 @@
 #include "hier_tile.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 
 namespace {
@@ -286,14 +285,6 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
 
 // ---- dK, dV (key-major) ------------------------------------------------------
 
-// LDS stages: Q[2] | dO[2] (rows and transposed) | per-query dwords[2] x
-// {mask, lse2, delta}, each stage its own __shared__ array (see QStages).
-struct KStages {
-  char* q[2];
-  char* d[2];
-  char* w[2];
-};
-
 template <int D>
 struct KCtx {
   const char* gq;
@@ -309,347 +300,235 @@ struct KCtx {
   bool active;
   Copier<D, kBothRead> cq;
   int row[Geo<D>::NC], tr[Geo<D>::NDB][2];
-  // key rows (vt: dk_kernel only) and the accumulator (dV^T or dK^T)
-  bf16x8 kt[Geo<D>::NC], vt[Geo<D>::NC];
+  // the wave's key rows (K^T or V^T operand) and its accumulator (dV^T or dK^T)
+  bf16x8 kt[Geo<D>::NC];
   f32x16 acc[Geo<D>::NDB];
   int ktok, kframe;
   bool valid;
   uint32_t bits;
 };
 
-template <int D>
-__device__ __forceinline__ void dk_copy(KCtx<D>& c, int t, const Idx<D>& ix, int qtok, char* stage_q,
-                                        char* stage_do, char* stage_w) {
-  copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, ix, stage_q, c.wave);
-  copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, ix, stage_do, c.wave);
-  copy_dwords(c.q_mask + t * kSlab, stage_w, c.lane);
-  dma4_lane(c.lse2 + qtok, stage_w + Geo<D>::MBYTES);
-  dma4_lane(c.delta + qtok, stage_w + 2 * Geo<D>::MBYTES);
-}
+// ---- dK and dV in one pass: wave pairs share S and P, pipelined over tiles ----
+//
+// Eight waves per workgroup over one key item of 128 rows; waves w (role A)
+// and w+4 (role B) own the same 32 key rows and run on the same SIMD.  Per
+// 64-query tile (two 32-query blocks):
+//   role A: S = Q K^T, P = exp2(S * c2 - lse2[q]) (0 where the query frame
+//           may not see the key frame), P to LDS (fp16), dV^T += dO^T P
+//   role B: dP = dO V^T, dS = P * (dP - delta[q]) with P from LDS,
+//           dK^T += Q^T dS
+// S is computed once for both gradients (four products per block, against
+// five for two separate passes).  Step t accumulates tile t (role A: dV from
+// the P it kept in registers; role B: dS and dK from the P role A wrote in
+// step t-1) while it computes S / P (role A) and dP (role B) of tile t+1, so
+// the products of the two roles and of the two tiles overlap on each SIMD;
+// one barrier per step hands P over.  Three LDS stages (tiles t, t+1 in use,
+// t+2 being copied), two P slots by tile parity; one workgroup per CU.
+// P travels as fp16 (10-bit mantissa; P <= 1): dK differs from a P kept in
+// fp32 by one rounding of P, dV is unchanged.
 
-// Query tile t of a key item: works on stage PAR while tile t+1 is copied into
-// stage PAR^1 in two bursts, Q (with the masks and the per-row lse and delta)
-// before the first 32-query block and dO before the second.
-template <int D, int PAR>
-__device__ __forceinline__ void dk_tile(KCtx<D>& c, int t, Idx<D>& inext, int& qnext,
-                                        const KStages& st) {
-  const bool more = t + 1 < c.nt;
-  if (more) {
-    copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, inext, st.q[PAR ^ 1], c.wave);
-    copy_dwords(c.q_mask + (t + 1) * kSlab, st.w[PAR ^ 1], c.lane);
-    dma4_lane(c.lse2 + qnext, st.w[PAR ^ 1] + Geo<D>::MBYTES);
-    dma4_lane(c.delta + qnext, st.w[PAR ^ 1] + 2 * Geo<D>::MBYTES);
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+constexpr int kPairWaves = 8;
+constexpr int kPairThreads = 64 * kPairWaves;
+
+template <int D>
+__global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int total) {
+  __shared__ __align__(16) char lds_q[3][Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_d[3][Geo<D>::TILEB];
+  __shared__ __align__(16) char lds_w[3][3 * Geo<D>::MBYTES];
+  // P of one query tile per wave pair (fp16): [tile parity][block][pair][half][lane]
+  __shared__ __align__(16) f16x8 lds_p[2 * 2 * 4 * 2 * 64];
+  const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
+  if (logical >= total) return;
+  const int head = logical / a.n_key_items;
+  const int item = logical - head * a.n_key_items;
+  const int32_t* it = a.key_items + (int64_t)item * 8;
+
+  KCtx<D> c;
+  const int tid = threadIdx.x;
+  c.lane = tid & 63;
+  const int wave8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool role_b = wave8 >= 4;
+  c.wave = wave8 & 3;
+  const int kbase = it[0], kstride = it[1], klen = it[2], row_start = it[3], row_count = it[4];
+  const int q_off = it[5], q_cnt = it[6];
+  c.nt = q_cnt / kSlab;
+  c.active = c.wave * 32 < row_count;
+  c.c2 = a.scale * kLog2e;
+  c.gq = reinterpret_cast<const char*>(a.q + (int64_t)head * a.q_sh);
+  c.gdo = reinterpret_cast<const char*>(a.dout + (int64_t)head * a.do_sh);
+  c.q_ss_b = (uint32_t)(a.q_ss * 2);
+  c.do_ss_b = (uint32_t)(a.do_ss * 2);
+  c.lse2 = a.lse2 + (int64_t)head * a.lse_stride_h;
+  c.delta = a.delta + (int64_t)head * a.lse_stride_h;
+  c.q_idx = a.key_q_idx + q_off;
+  c.q_mask = a.key_q_mask + q_off;
+  c.blk = a.key_blk_and + q_off / kSlab;
+  c.cq.init(c.wave, c.lane);
+#pragma unroll
+  for (int i = 0; i < Geo<D>::NC; ++i) c.row[i] = row_read_off<D, kBothRead>(c.lane, i);
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db) {
+    c.tr[db][0] = tr_read_off<D, kBothRead>(c.lane, db, 0);
+    c.tr[db][1] = tr_read_off<D, kBothRead>(c.lane, db, 1);
   }
-  {
-    const char* qs = st.q[PAR];
-    const char* ds_ = st.d[PAR];
-    const char* ws = st.w[PAR];
-    const uint32_t* mk = reinterpret_cast<const uint32_t*>(ws);
-    const float* l2 = reinterpret_cast<const float*>(ws + Geo<D>::MBYTES);
-    const float* dl = reinterpret_cast<const float*>(ws + 2 * Geo<D>::MBYTES);
+  const int r = c.wave * 32 + (c.lane & 31);
+  c.valid = r < row_count;
+  const int ri = row_start + (c.valid ? r : 0);
+  c.kframe = ri / klen;
+  c.ktok = kbase + c.kframe * kstride + (ri - c.kframe * klen);
+  if (role_b)
+    load_row<D>(c.kt, a.v + (int64_t)c.ktok * a.v_ss + (int64_t)head * a.v_sh, c.lane);
+  else
+    load_row<D>(c.kt, a.k + (int64_t)c.ktok * a.k_ss + (int64_t)head * a.k_sh, c.lane);
+#pragma unroll
+  for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c.acc[db][i] = 0.f;
+  f16x8* const pslot = lds_p + c.wave * 2 * 64 + c.lane;   // + par * 1024 + block * 512 + h * 64
+
+  auto copy_q_tile = [&](int t, const Idx<D>& ix, int qtok, int sg) {
+    if (role_b) {
+      copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, ix, lds_d[sg], c.wave);
+    } else {
+      copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, ix, lds_q[sg], c.wave);
+      if (c.wave == 0) copy_dwords(c.q_mask + t * kSlab, lds_w[sg], c.lane);
+      if (c.wave == 1) dma4_lane(c.lse2 + qtok, lds_w[sg] + Geo<D>::MBYTES);
+      if (c.wave == 2) dma4_lane(c.delta + qtok, lds_w[sg] + 2 * Geo<D>::MBYTES);
+    }
+  };
+  // role A: S and P of tile t (stage sg) into pb (bf16) and the P slot of parity par
+  auto a_front = [&](int sg, int par, bf16x8 (*pb)[2]) {
+    const uint32_t* mk = reinterpret_cast<const uint32_t*>(lds_w[sg]);
+    const float* l2 = reinterpret_cast<const float*>(lds_w[sg] + Geo<D>::MBYTES);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      if (qb == 1 && more) {
-        copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, inext, st.d[PAR ^ 1], c.wave);
-        const int tn = min(t + 2, c.nt - 1);
-        inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
-        qnext = c.q_idx[tn * kSlab + c.lane];
-      }
-      if (!c.active) continue;
-      const f32x16 s = row_mfma<D>(c.kt, qs, c.row, qb);
-      const f32x16 dp = row_mfma<D>(c.vt, ds_, c.row, qb);
-      bf16x8 ob[2];   // dS, bf16
+      f32x16 x = row_mfma<D>(c.kt, lds_q[sg], c.row, qb);
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
         const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[q0]);
         const u32x4 lw = *reinterpret_cast<const u32x4*>(&l2[q0]);
-        const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * g4 + e;
-          const uint32_t keep = keep_mask(w[e], c.kframe);
-          const float p = __uint_as_float(
-              __float_as_uint(__builtin_amdgcn_exp2f(fmaf(s[i], c.c2, -__uint_as_float(lw[e])))) & keep);
-          const float ds = __uint_as_float(__float_as_uint(p * (dp[i] - __uint_as_float(dw[e]))) & keep);
-          ob[i >> 3][i & 7] = (__bf16)ds;
+          x[i] = __uint_as_float(__float_as_uint(__builtin_amdgcn_exp2f(
+                                     fmaf(x[i], c.c2, -__uint_as_float(lw[e])))) &
+                                 keep_mask(w[e], c.kframe));
+          pb[qb][i >> 3][i & 7] = (__bf16)x[i];
         }
       }
-      // dK^T += Q^T dS
-      tr_mfma<D>(c.acc, ob, qs, c.tr, qb);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f16x8 ph;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ph[e] = (_Float16)x[8 * h + e];
+        pslot[par * 1024 + qb * 512 + h * 64] = ph;
+      }
     }
-  }
-  wait_copies();
-  __syncthreads();
-}
-
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void dk_kernel(HierBwdArgs a, int total) {
-  __shared__ __align__(16) char lds_q0[Geo<D>::TILEB], lds_q1[Geo<D>::TILEB];
-  __shared__ __align__(16) char lds_d0[Geo<D>::TILEB], lds_d1[Geo<D>::TILEB];
-  __shared__ __align__(16) char lds_w0[3 * Geo<D>::MBYTES], lds_w1[3 * Geo<D>::MBYTES];
-  const KStages st = {{lds_q0, lds_q1}, {lds_d0, lds_d1}, {lds_w0, lds_w1}};
-  const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
-  if (logical >= total) return;
-  const int head = logical / a.n_key_items;
-  const int item = logical - head * a.n_key_items;
-  const int32_t* it = a.key_items + (int64_t)item * 8;
-
-  KCtx<D> c;
-  const int tid = threadIdx.x;
-  c.lane = tid & 63;
-  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kbase = it[0], kstride = it[1], klen = it[2], row_start = it[3], row_count = it[4];
-  const int q_off = it[5], q_cnt = it[6];
-  c.nt = q_cnt / kSlab;
-  c.active = c.wave * 32 < row_count;
-  c.c2 = a.scale * kLog2e;
-  c.gq = reinterpret_cast<const char*>(a.q + (int64_t)head * a.q_sh);
-  c.gdo = reinterpret_cast<const char*>(a.dout + (int64_t)head * a.do_sh);
-  c.q_ss_b = (uint32_t)(a.q_ss * 2);
-  c.do_ss_b = (uint32_t)(a.do_ss * 2);
-  c.lse2 = a.lse2 + (int64_t)head * a.lse_stride_h;
-  c.delta = a.delta + (int64_t)head * a.lse_stride_h;
-  c.q_idx = a.key_q_idx + q_off;
-  c.q_mask = a.key_q_mask + q_off;
-  c.blk = a.key_blk_and + q_off / kSlab;
-  c.cq.init(c.wave, c.lane);
+  };
+  // role B: dS of tile t from its P slot and dp, then dK^T += Q^T dS
+  auto b_back = [&](int sg, int par, const f32x16* dp) {
+    const float* dl = reinterpret_cast<const float*>(lds_w[sg] + 2 * Geo<D>::MBYTES);
 #pragma unroll
-  for (int i = 0; i < Geo<D>::NC; ++i) c.row[i] = row_read_off<D, kBothRead>(c.lane, i);
+    for (int qb = 0; qb < 2; ++qb) {
+      bf16x8 ob[2];
 #pragma unroll
-  for (int db = 0; db < Geo<D>::NDB; ++db) {
-    c.tr[db][0] = tr_read_off<D, kBothRead>(c.lane, db, 0);
-    c.tr[db][1] = tr_read_off<D, kBothRead>(c.lane, db, 1);
-  }
+      for (int h = 0; h < 2; ++h) {
+        const f16x8 ph = pslot[par * 1024 + qb * 512 + h * 64];
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+          const int g4 = 2 * h + g2;
+          const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
+          const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * g4 + e;
+            ob[i >> 3][i & 7] = (__bf16)((float)ph[4 * g2 + e] * (dp[qb][i] - __uint_as_float(dw[e])));
+          }
+        }
+      }
+      tr_mfma<D>(c.acc, ob, lds_q[sg], c.tr, qb);   // dK^T += Q^T dS
+    }
+  };
 
-  // the lane's key row
-  const int r = c.wave * 32 + (c.lane & 31);
-  c.valid = r < row_count;
-  const int ri = row_start + (c.valid ? r : 0);
-  c.kframe = ri / klen;
-  c.ktok = kbase + c.kframe * kstride + (ri - c.kframe * klen);
-  c.bits = wave_or(c.valid ? (1u << c.kframe) : 0u);
-  load_row<D>(c.kt, a.k + (int64_t)c.ktok * a.k_ss + (int64_t)head * a.k_sh, c.lane);
-  load_row<D>(c.vt, a.v + (int64_t)c.ktok * a.v_ss + (int64_t)head * a.v_sh, c.lane);
-#pragma unroll
-  for (int db = 0; db < Geo<D>::NDB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) c.acc[db][i] = 0.f;
-
+  auto run = [&](auto rb) {
+    constexpr bool RB = decltype(rb)::value;
   const int nt = c.nt;
   if (nt > 0) {
+    // prologue: tiles 0 and 1 resident; S / P of tile 0 (role A, P slot 0),
+    // dP of tile 0 (role B)
     const Idx<D> i0 = load_idx<D>(c.q_idx, 0, c.cq.idx_off);
-    dk_copy<D>(c, 0, i0, c.q_idx[c.lane], st.q[0], st.d[0], st.w[0]);
-    const int tn = min(1, nt - 1);
-    Idx<D> inext = load_idx<D>(c.q_idx, tn, c.cq.idx_off);
-    int qnext = c.q_idx[tn * kSlab + c.lane];
-    wait_copies();
-    __syncthreads();
-    int t = 0;
-    for (; t + 1 < nt; t += 2) {
-      dk_tile<D, 0>(c, t, inext, qnext, st);
-      dk_tile<D, 1>(c, t + 1, inext, qnext, st);
-    }
-    if (t < nt) dk_tile<D, 0>(c, t, inext, qnext, st);
-  }
-  if (c.active && c.valid)
-    store_acc<D>(a.dk + (int64_t)c.ktok * a.dk_ss + (int64_t)head * a.dk_sh, c.acc, a.scale, c.lane);
-}
-
-// ---- dV pass, software-pipelined ---------------------------------------------
-//
-// The forward's three-stage pipeline over 32-query blocks of a key item's
-// list (one step: three independent streams, which the compiler interleaves
-// by itself -- explicit sched_group_barrier patterns measured no faster):
-//     step j:  S(j+2) = Q K^T  ||  P(j+1) = exp2(S')  ||  dV^T(j) += dO^T P(j)
-// with S' = S * scale * log2(e) - lse2[q], the query frames that may not see
-// the lane's key frame at -inf, applied at the end of the step that computes
-// S (the per-query lse2 / mask words follow the Q tiles through LDS).  While
-// the two blocks of query tile t are accumulated, Q tile t+2 (with its words)
-// and dO tile t+1 are in flight.
-
-template <int D>
-__device__ __forceinline__ void dv_prep(const KCtx<D>& c, f32x16& s, const char* wslot, int kb,
-                                        bool need) {
-  const uint32_t* mk = reinterpret_cast<const uint32_t*>(wslot);
-  const float* l2 = reinterpret_cast<const float*>(wslot + Geo<D>::MBYTES);
-#pragma unroll
-  for (int g4 = 0; g4 < 4; ++g4) {
-    const int q0 = kb * 32 + 8 * g4 + 4 * (c.lane >> 5);
-    const u32x4 lw = *reinterpret_cast<const u32x4*>(&l2[q0]);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s[4 * g4 + e] = fmaf(s[4 * g4 + e], c.c2, -__uint_as_float(lw[e]));
-  }
-  if (need) {
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int q0 = kb * 32 + 8 * g4 + 4 * (c.lane >> 5);
-      const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[q0]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t keep = keep_mask(w[e], c.kframe);
-        const uint32_t x = __float_as_uint(s[4 * g4 + e]);
-        s[4 * g4 + e] = __uint_as_float((x & keep) | (0xff800000u & ~keep));
-      }
-    }
-  }
-}
-
-__device__ __forceinline__ void dv_p(const f32x16& s, bf16x8* p) {
-#pragma unroll
-  for (int i = 0; i < 16; ++i) p[i >> 3][i & 7] = (__bf16)__builtin_amdgcn_exp2f(s[i]);
-}
-
-// Step j = 2t + B: S of block B of Q tile t+1 into sq (stage PAR^1), P of
-// block j+1 (sc) into pn, dV of block B of dO tile t (stage PAR) with pv;
-// then sq turned into S' with the words of tile t+1 (need_next: some query
-// of that tile may not see a key frame of the wave).
-template <int D, int PAR, int B>
-__device__ __forceinline__ void dv_half(KCtx<D>& c, f32x16& sq, const f32x16& sc, const bf16x8* pv,
-                                        bf16x8* pn, bool need_next, const KStages& st) {
-  sq = row_mfma<D>(c.kt, st.q[PAR ^ 1], c.row, B);
-  dv_p(sc, pn);
-  tr_mfma<D>(c.acc, pv, st.d[PAR], c.tr, B);
-  asm volatile("" : "+v"(pn[0]), "+v"(pn[1]));
-  dv_prep<D>(c, sq, st.w[PAR ^ 1], B, need_next);
-}
-
-__device__ __forceinline__ bool dv_need(uint32_t blk, uint32_t bits) { return (blk & bits) != bits; }
-
-// Query tile iteration t (t + 1 < nt): copies Q(t+2) and its words into stage
-// PAR, runs step 2t, copies dO(t+1) into stage PAR^1, runs step 2t+1.
-// Invariant on entry: Q(t+1) with its words and dO(t) resident; S'(2t+1) (sb)
-// ready; P(2t) (pa) ready; iq / id the indices of tiles min(t+2, nt-1) /
-// t+1, qn the query rows of tile min(t+2, nt-1), blk the flags of tile t+1.
-template <int D, int PAR>
-__device__ __forceinline__ void dv_iter(KCtx<D>& c, int t, f32x16& sa, f32x16& sb, bf16x8* pa,
-                                        bf16x8* pb, Idx<D>& iq, Idx<D>& id, int& qn, uint32_t& blk,
-                                        const KStages& st) {
-  if (t + 2 < c.nt) {
-    copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, iq, st.q[PAR], c.wave);
-    if (c.wave == 0) copy_dwords(c.q_mask + (t + 2) * kSlab, st.w[PAR], c.lane);
-    if (c.wave == 1) dma4_lane(c.lse2 + qn, st.w[PAR] + Geo<D>::MBYTES);
-  }
-  const int t3 = min(t + 3, c.nt - 1);
-  iq = load_idx<D>(c.q_idx, t3, c.cq.idx_off);
-  qn = c.q_idx[t3 * kSlab + c.lane];
-  const uint32_t blk_pre = c.blk[min(t + 2, c.nt - 1)];
-  const bool need = dv_need(blk, c.bits);
-  if (c.active) dv_half<D, PAR, 0>(c, sa, sb, pa, pb, need, st);
-  copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, id, st.d[PAR ^ 1], c.wave);
-  id = load_idx<D>(c.q_idx, min(t + 2, c.nt - 1), c.cq.idx_off);
-  if (c.active) dv_half<D, PAR, 1>(c, sb, sa, pb, pa, need, st);
-  wait_copies();
-  __syncthreads();
-  blk = blk_pre;
-}
-
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void dv_kernel(HierBwdArgs a, int total) {
-  __shared__ __align__(16) char lds_q0[Geo<D>::TILEB], lds_q1[Geo<D>::TILEB];
-  __shared__ __align__(16) char lds_d0[Geo<D>::TILEB], lds_d1[Geo<D>::TILEB];
-  __shared__ __align__(16) char lds_w0[2 * Geo<D>::MBYTES], lds_w1[2 * Geo<D>::MBYTES];
-  const KStages st = {{lds_q0, lds_q1}, {lds_d0, lds_d1}, {lds_w0, lds_w1}};
-  const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
-  if (logical >= total) return;
-  const int head = logical / a.n_key_items;
-  const int item = logical - head * a.n_key_items;
-  const int32_t* it = a.key_items + (int64_t)item * 8;
-
-  KCtx<D> c;
-  const int tid = threadIdx.x;
-  c.lane = tid & 63;
-  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kbase = it[0], kstride = it[1], klen = it[2], row_start = it[3], row_count = it[4];
-  const int q_off = it[5], q_cnt = it[6];
-  c.nt = q_cnt / kSlab;
-  c.active = c.wave * 32 < row_count;
-  c.c2 = a.scale * kLog2e;
-  c.gq = reinterpret_cast<const char*>(a.q + (int64_t)head * a.q_sh);
-  c.gdo = reinterpret_cast<const char*>(a.dout + (int64_t)head * a.do_sh);
-  c.q_ss_b = (uint32_t)(a.q_ss * 2);
-  c.do_ss_b = (uint32_t)(a.do_ss * 2);
-  c.lse2 = a.lse2 + (int64_t)head * a.lse_stride_h;
-  c.delta = a.delta + (int64_t)head * a.lse_stride_h;
-  c.q_idx = a.key_q_idx + q_off;
-  c.q_mask = a.key_q_mask + q_off;
-  c.blk = a.key_blk_and + q_off / kSlab;
-  c.cq.init(c.wave, c.lane);
-#pragma unroll
-  for (int i = 0; i < Geo<D>::NC; ++i) c.row[i] = row_read_off<D, kBothRead>(c.lane, i);
-#pragma unroll
-  for (int db = 0; db < Geo<D>::NDB; ++db) {
-    c.tr[db][0] = tr_read_off<D, kBothRead>(c.lane, db, 0);
-    c.tr[db][1] = tr_read_off<D, kBothRead>(c.lane, db, 1);
-  }
-  const int r = c.wave * 32 + (c.lane & 31);
-  c.valid = r < row_count;
-  const int ri = row_start + (c.valid ? r : 0);
-  c.kframe = ri / klen;
-  c.ktok = kbase + c.kframe * kstride + (ri - c.kframe * klen);
-  c.bits = wave_or(c.valid ? (1u << c.kframe) : 0u);
-  load_row<D>(c.kt, a.k + (int64_t)c.ktok * a.k_ss + (int64_t)head * a.k_sh, c.lane);
-#pragma unroll
-  for (int db = 0; db < Geo<D>::NDB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) c.acc[db][i] = 0.f;
-
-  const int nt = c.nt;
-  if (nt > 0) {
-    // prologue: Q(0), dO(0), Q(1) and the words of tiles 0, 1 resident; S'(0),
-    // S'(1) computed; P(0) from S'(0)
-    {
-      const Idx<D> i0 = load_idx<D>(c.q_idx, 0, c.cq.idx_off);
-      copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, i0, st.q[0], c.wave);
-      copy_tile<D, kBothRead>(c.gdo, c.do_ss_b, c.cq, i0, st.d[0], c.wave);
-      if (c.wave == 0) copy_dwords(c.q_mask, st.w[0], c.lane);
-      if (c.wave == 1) dma4_lane(c.lse2 + c.q_idx[c.lane], st.w[0] + Geo<D>::MBYTES);
-      if (nt > 1) {
-        const Idx<D> i1 = load_idx<D>(c.q_idx, 1, c.cq.idx_off);
-        copy_tile<D, kBothRead>(c.gq, c.q_ss_b, c.cq, i1, st.q[1], c.wave);
-        if (c.wave == 0) copy_dwords(c.q_mask + kSlab, st.w[1], c.lane);
-        if (c.wave == 1) dma4_lane(c.lse2 + c.q_idx[kSlab + c.lane], st.w[1] + Geo<D>::MBYTES);
-      }
+    copy_q_tile(0, i0, c.q_idx[c.lane], 0);
+    if (nt > 1) {
+      const Idx<D> i1 = load_idx<D>(c.q_idx, 1, c.cq.idx_off);
+      copy_q_tile(1, i1, c.q_idx[kSlab + c.lane], 1);
     }
     const int t2 = min(2, nt - 1);
-    Idx<D> iq = load_idx<D>(c.q_idx, t2, c.cq.idx_off);
-    int qn = c.q_idx[t2 * kSlab + c.lane];
-    Idx<D> id = load_idx<D>(c.q_idx, min(1, nt - 1), c.cq.idx_off);
-    uint32_t blk = c.blk[min(1, nt - 1)];
+    Idx<D> inext = load_idx<D>(c.q_idx, t2, c.cq.idx_off);
+    int qnext = c.q_idx[t2 * kSlab + c.lane];
     wait_copies();
     __syncthreads();
-    f32x16 sa, sb;
-    bf16x8 pa[2], pb[2];
+    bf16x8 pb[2][2];   // role A: P of the current tile (the dV operand)
+    f32x16 dp[2];      // role B: dP of the current tile
     if (c.active) {
-      const bool need0 = dv_need(c.blk[0], c.bits);
-      sa = row_mfma<D>(c.kt, st.q[0], c.row, 0);
-      sb = row_mfma<D>(c.kt, st.q[0], c.row, 1);
-      dv_prep<D>(c, sa, st.w[0], 0, need0);
-      dv_prep<D>(c, sb, st.w[0], 1, need0);
-      dv_p(sa, pa);
-    }
-    __syncthreads();   // every wave has read Q stage 0 and words stage 0
-    int t = 0;
-    for (; t + 2 < nt; t += 2) {
-      dv_iter<D, 0>(c, t, sa, sb, pa, pb, iq, id, qn, blk, st);
-      dv_iter<D, 1>(c, t + 1, sa, sb, pa, pb, iq, id, qn, blk, st);
-    }
-    // last tile t = nt - 1: P of its block 1 (sb), dV of both blocks
-    if (t + 1 < nt) {
-      dv_iter<D, 0>(c, t, sa, sb, pa, pb, iq, id, qn, blk, st);
-      if (c.active) {
-        dv_p(sb, pb);
-        tr_mfma<D>(c.acc, pa, st.d[1], c.tr, 0);
-        tr_mfma<D>(c.acc, pb, st.d[1], c.tr, 1);
+      if constexpr (!RB) a_front(0, 0, pb);
+      else {
+        dp[0] = row_mfma<D>(c.kt, lds_d[0], c.row, 0);
+        dp[1] = row_mfma<D>(c.kt, lds_d[0], c.row, 1);
       }
-    } else if (c.active) {
-      dv_p(sb, pb);
-      tr_mfma<D>(c.acc, pa, st.d[0], c.tr, 0);
-      tr_mfma<D>(c.acc, pb, st.d[0], c.tr, 1);
     }
+    hier::barrier_lds();   // P of tile 0 written
+    // iteration t: tiles t (stage s0) and t+1 (s1) resident, P(t) in slot t&1;
+    // copies of tile t+2 into s2; role A: S / P of tile t+1 and dV of tile t;
+    // role B: dP of tile t+1 and dS / dK of tile t
+    int s0 = 0, s1 = 1, s2 = 2;
+    // one step; `next` (a constant at both call sites) says whether tile t+1
+    // exists, so the steady-state steps carry no branch around the products
+    auto step = [&](int t, bool next) {
+      if (t + 2 < nt) {
+        copy_q_tile(t + 2, inext, qnext, s2);
+        const int t3 = min(t + 3, nt - 1);
+        inext = load_idx<D>(c.q_idx, t3, c.cq.idx_off);
+        qnext = c.q_idx[t3 * kSlab + c.lane];
+      }
+      if (c.active) {
+        if constexpr (!RB) {
+          bf16x8 pn[2][2];
+          if (next) a_front(s1, (t + 1) & 1, pn);
+          tr_mfma<D>(c.acc, pb[0], lds_d[s0], c.tr, 0);   // dV^T += dO^T P
+          tr_mfma<D>(c.acc, pb[1], lds_d[s0], c.tr, 1);
+          if (next) {
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) { pb[qb][0] = pn[qb][0]; pb[qb][1] = pn[qb][1]; }
+          }
+        } else {
+          f32x16 dn[2];
+          if (next) {
+            dn[0] = row_mfma<D>(c.kt, lds_d[s1], c.row, 0);
+            dn[1] = row_mfma<D>(c.kt, lds_d[s1], c.row, 1);
+          }
+          b_back(s0, t & 1, dp);
+          if (next) { dp[0] = dn[0]; dp[1] = dn[1]; }
+        }
+      }
+      wait_copies();
+      __syncthreads();
+      const int sx = s0; s0 = s1; s1 = s2; s2 = sx;
+    };
+    int t = 0;
+    for (; t + 1 < nt; ++t) step(t, true);
+    step(t, false);
   }
-  if (c.active && c.valid)
-    store_acc<D>(a.dv + (int64_t)c.ktok * a.dv_ss + (int64_t)head * a.dv_sh, c.acc, 1.f, c.lane);
+  };
+  if (role_b) run(std::true_type{});
+  else run(std::false_type{});
+  if (c.active && c.valid) {
+    if (role_b)
+      store_acc<D>(a.dk + (int64_t)c.ktok * a.dk_ss + (int64_t)head * a.dk_sh, c.acc, a.scale, c.lane);
+    else
+      store_acc<D>(a.dv + (int64_t)c.ktok * a.dv_ss + (int64_t)head * a.dv_sh, c.acc, 1.f, c.lane);
+  }
 }
 
 // ---- membership STE partial sums (query-major, gated keys only) -------------
@@ -915,14 +794,11 @@ int bwd_run(const HierBwdArgs& a, void* stream) {
   }
   if (tk > 0) {
     const int grid = (int)hier::xcd_grid(tk);
-    if (a.D == 128) {
-      hipLaunchKernelGGL(dv_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
-      hipLaunchKernelGGL(dk_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
-    } else {
-      hipLaunchKernelGGL(dv_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
-      hipLaunchKernelGGL(dk_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)tk);
-    }
-    int rc = hier::check_launch("dv_kernel / dk_kernel");
+    if (a.D == 128)
+      hipLaunchKernelGGL(dkv_kernel<128>, dim3(grid), dim3(kPairThreads), 0, s, a, (int)tk);
+    else
+      hipLaunchKernelGGL(dkv_kernel<64>, dim3(grid), dim3(kPairThreads), 0, s, a, (int)tk);
+    int rc = hier::check_launch("dkv_kernel");
     if (rc != HIER_OK) return rc;
   }
   const int64_t ts = (int64_t)a.n_ste_items * a.H;

@@ -31,6 +31,13 @@ inline int check_launch(const char* what) {
   return HIER_OK;
 }
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations,
+// not for its outstanding global loads or LDS copies (__syncthreads' fence
+// would wait for those too).
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 }  // namespace hier
 
 #define HIER_REQUIRE(cond, code, ...) \

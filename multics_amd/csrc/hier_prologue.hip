@@ -93,14 +93,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
-// Workgroup barrier for LDS data only: waits for this wave's LDS operations,
-// not for its outstanding global loads (__syncthreads' workgroup fence would
-// wait for those too, so that the next trip's prefetched projections would
-// land before the barrier instead of during the trip).
-__device__ __forceinline__ void barrier_lds() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // Sums of NV values over the workgroup.  Full waves (blockDim a multiple of
 // 64): a register reduction per wave, then the wave sums through red, laid
 // out [parity][NV][16 waves] with the slots of absent waves zero (the caller
@@ -117,7 +109,7 @@ __device__ __forceinline__ void block_sum(float* v, float* red, int parity) {
     if ((threadIdx.x & 63) == 0)
 #pragma unroll
       for (int i = 0; i < NV; ++i) r[i * 16 + (threadIdx.x >> 6)] = v[i];
-    barrier_lds();
+    hier::barrier_lds();   // (not __syncthreads: the next trip's prefetch stays in flight)
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const float4* r4 = reinterpret_cast<const float4*>(r + i * 16);
