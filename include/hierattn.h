@@ -132,8 +132,8 @@ int hier_meta_build(const HierTopo* topo, const HierMetaOut* out, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Backward lists derived on the device from a full-sequence tile list:     */
-/* the key-major list of the dK / dV passes and the membership-STE list,    */
-/* bit for bit the host builders transpose_tiles / ste_tiles of             */
+/* the key-major list of the dK / dV pass and the membership-STE list, bit  */
+/* for bit the host builders transpose_tiles_host / ste_tiles_host of       */
 /* multics_amd/metadata.py.  No reference counterpart: the reference's      */
 /* backward is FlexAttention's autograd over its BlockMask                  */
 /* (multics/models/attention.py:322-353, 367-434).                          */
