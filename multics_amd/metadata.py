@@ -128,6 +128,10 @@ class BlockTopology:
     tile_qbase: list = None
     ref_qstride: tuple = (0, 0, 0)
     tile_qstride: tuple = (0, 0, 0)
+    # set by full_sequence_topology, whose frame lists satisfy the per-row
+    # checks of validate() by construction (kept = [b1 - W - n, b1) clipped
+    # at 0, which holds the block's query frames since W >= n)
+    frames_valid: bool = False
 
     @property
     def B(self) -> int:
@@ -144,6 +148,11 @@ class BlockTopology:
         if self.no_local and self.KL != 0:
             raise ValueError("hier_no_local_hub metadata requires K_L=0 and empty local caches")
         T_mem = None if self.membership is None else self.membership.shape[0]
+        if self.frames_valid:
+            last = max((f for qf in self.q_frames for f in qf), default=0)
+            if T_mem is not None and last >= T_mem:
+                raise ValueError(f"membership T={T_mem} does not cover the cached frames")
+            return
         for b in range(self.B):
             af = self.agent_frames[b]
             if len(af) != P or any(len(x) != len(af[0]) for x in af):
@@ -276,7 +285,7 @@ def full_sequence_topology(*, P, T, L, N, KL, KG, n, window, direct, labels=None
         labels=LB if lab is not None else None, membership=mem, global_only=go,
         ref_agent_base=A, ref_local_base=Lo, ref_global_base=G,
         tile_agent_base=A, tile_local_base=Lo, tile_global_base=G,
-        ref_qbase=RQ, tile_qbase=RQ, ref_qstride=stride, tile_qstride=stride)
+        ref_qbase=RQ, tile_qbase=RQ, ref_qstride=stride, tile_qstride=stride, frames_valid=True)
 
 
 # --------------------------------------------------------------------------
