@@ -325,7 +325,6 @@ struct KCtx {
   const float* delta;
   const int32_t* q_idx;
   const uint32_t* q_mask;
-  const uint32_t* blk;
   uint32_t q_ss_b, do_ss_b;
   float c2;
   int nt, wave, lane;
@@ -337,7 +336,6 @@ struct KCtx {
   f32x16 acc[Geo<D>::NDB];
   int ktok, kframe;
   bool valid;
-  uint32_t bits;
 };
 
 // ---- dK and dV in one pass: wave pairs share S and P, pipelined over tiles ----
@@ -395,7 +393,6 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
   c.delta = a.delta + (int64_t)head * a.lse_stride_h;
   c.q_idx = a.key_q_idx + q_off;
   c.q_mask = a.key_q_mask + q_off;
-  c.blk = a.key_blk_and + q_off / kSlab;
   c.cq.init(c.wave, c.lane);
 #pragma unroll
   for (int i = 0; i < Geo<D>::NC; ++i) c.row[i] = row_read_off<D, kBothRead>(c.lane, i);
