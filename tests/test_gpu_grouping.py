@@ -1,7 +1,7 @@
 """The membership producer feeding the attention path end to end.
 
-Labels generated from a bundled tick state (the P6 synthetic fixture, whose
-groups change between periods, and a real 4-player clip) give the
+Labels generated from a bundled tick state (the P6 and P10 synthetic
+fixtures, whose groups change between periods, and a real 4-player clip) give the
 ``membership`` / ``global_only`` topology; the HIP metadata builder turns it
 into a tile list, the forward runs on it at the C2 / C3 geometry (220 tokens
 per player-frame, 42 latent frames, window 21), and sampled rows are compared
@@ -31,7 +31,7 @@ GOLD = Path(__file__).parent / "golden" / "grouping"
 MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
 
-@pytest.mark.parametrize("case", ["p6_moving_pairs", "example_4_01"])
+@pytest.mark.parametrize("case", ["p6_moving_pairs", "p10_moving_pairs", "example_4_01"])
 def test_generated_membership_drives_the_forward(case):
     need_gpu()
     state = GroupingState.load(GOLD / f"{case}.state.npz")
