@@ -200,3 +200,28 @@ def test_label_file_round_trip_and_topology_inputs(example, tmp_path):
     assert mem.shape == (42, 2, 4) and go.shape == (42, 4)
     # what the mask builders read: every player is a member or global-only
     assert ((mem.any(1) ^ go) | ~got["eligible"][None]).all()
+
+
+def test_eight_player_labels_satisfy_the_generated_schema(example):
+    """No golden labels exist at P8: a state of two copies of the bundled
+    4-player clip (the copy moved 3000 units away, so the halves never see
+    each other) must give labels that pass every generated-schema check, with
+    each semantic group (positive score) inside one half; groups made by the
+    idle-slot recovery (negative score) have no score floor and may span."""
+    state, four = example
+    pos = np.concatenate([state.pos, state.pos + np.float32(3000.0)], axis=1)
+    eight = replace(state, pos=pos, yaw=np.concatenate([state.yaw] * 2, axis=1),
+                    pitch=np.concatenate([state.pitch] * 2, axis=1),
+                    alive=np.concatenate([state.alive] * 2, axis=1),
+                    present=np.concatenate([state.present] * 2, axis=1),
+                    player_slots=np.arange(8, dtype=np.int64))
+    got = generate_labels(eight)
+    validate_generated_labels({k: torch.from_numpy(v) for k, v in got.items()}, 8)
+    assert got["period_membership"].shape == (4, 3, 8)
+    for frame, scores in zip(got["period_membership"], got["period_scores"]):
+        for slot, score in zip(frame, scores):
+            members = np.nonzero(slot)[0]
+            if score > 0:
+                assert (members < 4).all() or (members >= 4).all()
+    # each half alone is the 4-player clip: its best semantic group scores the same
+    np.testing.assert_array_equal(got["period_scores"].max(1), four["period_scores"].max(1))
