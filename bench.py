@@ -268,13 +268,14 @@ def bench_training(dev, steps=10, warmup=3):
     def rebuild():
         """The lists of the current logits, built from scratch (no cache):
         membership read back, both device metadata passes, both device
-        backward-list passes."""
+        key-major passes and the STE classes of the forward list."""
         from multics_amd import metadata as M
         m = (lg.detach() > 0).cpu().numpy()
         t_ = M.build(M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
                                               direct=True, membership=m, global_only=~m.any(1)),
                      dev).tiles
-        M.backward_lists(t_, geo)
+        M.backward_lists(t_, None)
+        M.ste_classes(t_, geo)
         return t_
 
     def step_rebuild():
@@ -296,9 +297,10 @@ def bench_training(dev, steps=10, warmup=3):
             "ms_fwd_bwd_with_rebuild": round(ms_step_rebuild, 4),
             "useful_tflops_fwd_bwd": round((flop_f + flop_b) / (ms_step * 1e-3) / 1e12, 2),
             "useful_tflops_bwd": round(flop_b / (ms_bwd * 1e-3) / 1e12, 2),
-            "note": "bwd = dQ (query-major) + dK/dV (key-major) + membership STE pass; "
+            "note": "bwd = dQ (query-major, with the membership STE sums) + dK/dV (key-major); "
                     "useful FLOP 4*H*D*E fwd, 10*H*D*E bwd; *_rebuild: every step rebuilds "
-                    "the forward, key-major and STE lists from the logits on the device "
+                    "the forward and key-major lists and the STE classes from the logits on "
+                    "the device "
                     "(membership read back, two count read-backs), as a step whose logits "
                     "flipped membership must"}
 

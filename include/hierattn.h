@@ -175,6 +175,13 @@ int64_t hier_derive_workspace(const HierDeriveArgs* args);
 int hier_derive_count(const HierDeriveArgs* args, void* stream);
 /* Pass 2: the two lists, their per-64 mask ANDs and their items.            */
 int hier_derive_build(const HierDeriveArgs* args, void* stream);
+/* Membership-STE class of every entry of the forward list (n_items, kv_len, */
+/* P..KL, items, kv_idx, kv_mask of args; no workspace, no pass 1): g for a */
+/* local-hub key of group g in a player group's list, p for a key of player */
+/* p in a local-hub group's list, -1 for every other entry and for masks of */
+/* 0 -- the selection of the STE list, kept in forward-list order.  Input   */
+/* tile_kv_class of hier_attn_bwd.                                          */
+int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Q/K/V layout prologue: camera-pose Q/K adapter, RMSNorm over all heads,  */
@@ -290,6 +297,12 @@ typedef struct HierBwdArgs {
   const int32_t* ste_kv_class;
   float* ste_partial;              /* [H][ste_rows][16]                        */
   int64_t ste_stride_h;            /* elements between heads of ste_partial    */
+  /* Optional membership STE inside the dQ pass (instead of an STE list,    */
+  /* n_ste_items must then be 0): the class of every entry of the forward    */
+  /* list (hier_derive_ste_classes; -1 or >= 16 = no gating bit).  The dQ    */
+  /* pass adds dS over each row's entries of class c into                    */
+  /* ste_partial[h][row][c] and writes it for every row of every item.       */
+  const int32_t* tile_kv_class;
 } HierBwdArgs;
 
 int hier_attn_bwd(const HierBwdArgs* args, void* stream);

@@ -98,16 +98,63 @@ __device__ __forceinline__ uint32_t keep_mask(uint32_t bits, int bit) {
   return (uint32_t)__builtin_amdgcn_sbfe((int)bits, bit, 1);   // 0 or ~0
 }
 
+// ---- membership STE sums -----------------------------------------------------
+
+constexpr int kSteClasses = 16;
+constexpr int kSteSlots = kWaves * 32;   // one slot per (class, query row of a workgroup)
+
+// Adds a lane's 16 dS terms of one 32-key block into the slots of their
+// classes, acc[class * kSteSlots]; a class outside [0, kSteClasses) marks a
+// key whose edge no membership bit gates, and is skipped.  The keys of a
+// block mostly share one class (lists keep each class's keys together): a
+// lane whose 16 keys do adds their sum once, otherwise each term.  Only the
+// two lanes of a query row (its two key halves) share a slot.
+__device__ __forceinline__ void ste_add(float* acc, const float* ds, const uint32_t* cls,
+                                        bool valid) {
+  bool same = true;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) same = same && cls[i] == cls[0];
+  if (!valid) return;
+  if (same) {
+    if (cls[0] < kSteClasses) {
+      float t = ds[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) t += ds[i];
+      atomicAdd(&acc[cls[0] * kSteSlots], t);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (cls[i] < kSteClasses) atomicAdd(&acc[cls[i] * kSteSlots], ds[i]);
+  }
+}
+
+// The same for 4 keys (the dQ pass, whose registers are nearly all taken).
+__device__ __forceinline__ void ste_add4(float* acc, const float* ds, const u32x4& cls,
+                                         bool valid) {
+  const bool same = cls[1] == cls[0] && cls[2] == cls[0] && cls[3] == cls[0];
+  if (!valid) return;
+  if (same) {
+    if (cls[0] < kSteClasses) atomicAdd(&acc[cls[0] * kSteSlots], (ds[0] + ds[1]) + (ds[2] + ds[3]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (cls[e] < kSteClasses) atomicAdd(&acc[cls[e] * kSteSlots], ds[e]);
+  }
+}
+
 // ---- dQ (query-major) --------------------------------------------------------
 
-// LDS stages: K[2] (rows and transposed) | V[2] (rows) | masks[2], each its
-// own __shared__ array.  Distinct arrays let the compiler see that the copies
-// into one stage never alias the reads of the other; given one array it waits
-// for every outstanding copy before the first LDS read that follows them.
+// LDS stages: K[2] (rows and transposed) | V[2] (rows) | masks[2] | STE
+// classes[2] (membership STE only), each its own __shared__ array.  Distinct
+// arrays let the compiler see that the copies into one stage never alias the
+// reads of the other; given one array it waits for every outstanding copy
+// before the first LDS read that follows them.
 struct QStages {
   char* k[2];
   char* v[2];
   char* m[2];
+  char* c[2];
 };
 
 template <int D>
@@ -117,6 +164,8 @@ struct QCtx {
   const char* gv;
   const int32_t* kv_idx;
   const uint32_t* kv_mask;
+  const int32_t* kv_cls;       // STE class of each list entry (membership STE only)
+  float* ste;                  // the lane's row's STE slots, ste[class * kSteSlots]
   uint32_t k_ss_b, v_ss_b;
   float c2;
   int nt, wave, lane;
@@ -155,20 +204,25 @@ __device__ __forceinline__ void p_exp(f32x16& s, float c2, float lse2) {
 }
 
 // dS^T = P^T (dP^T - delta) of block kb, the keys the lane's query frame may
-// not see zeroed, rounded to the bf16 operand of the dQ product.
+// not see zeroed, rounded to the bf16 operand of the dQ product.  With STE,
+// the fp32 dS of the block's gated keys (class words `cl`, from LDS) is also
+// added into the row's class slots.
+template <bool STE>
 __device__ __forceinline__ void ds_block(const f32x16& p, const f32x16& dp, float delta,
-                                         const uint32_t* mk, int kb, int qframe, int lane,
-                                         bf16x8* dsb) {
+                                         const uint32_t* mk, const uint32_t* cl, float* ste,
+                                         bool valid, int kb, int qframe, int lane, bf16x8* dsb) {
 #pragma unroll
   for (int g4 = 0; g4 < 4; ++g4) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[kb * 32 + 8 * g4 + 4 * (lane >> 5)]);
+    const int k0 = kb * 32 + 8 * g4 + 4 * (lane >> 5);
+    const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[k0]);
+    float ds[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 4 * g4 + e;
-      const float ds = __uint_as_float(__float_as_uint(p[i] * (dp[i] - delta)) &
-                                       keep_mask(w[e], qframe));
-      dsb[i >> 3][i & 7] = (__bf16)ds;
+      ds[e] = __uint_as_float(__float_as_uint(p[i] * (dp[i] - delta)) & keep_mask(w[e], qframe));
+      dsb[i >> 3][i & 7] = (__bf16)ds[e];
     }
+    if constexpr (STE) ste_add4(ste, ds, *reinterpret_cast<const u32x4*>(&cl[k0]), valid);
   }
 }
 
@@ -182,12 +236,15 @@ __device__ __forceinline__ void ds_block(const f32x16& p, const f32x16& dp, floa
 //     dP(1) || exp S(1) ; dQ(0) || dS(1) ; dQ(1)
 // (the masks are applied to every block: 16 ANDs under the MFMAs are cheaper
 // than a branch, which would split the schedule).
-template <int D, int PAR>
+// STE: the STE class words travel with the masks (the tile itself has no
+// gated key; dq_tile_ste handles those).
+template <int D, int PAR, bool STE>
 __device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, const QStages& st) {
   const bool more = t + 1 < c.nt;
   if (more) {
     copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, st.k[PAR ^ 1], c.wave);
     copy_dwords(c.kv_mask + (t + 1) * kSlab, st.m[PAR ^ 1], c.lane);
+    if constexpr (STE) copy_dwords(c.kv_cls + (t + 1) * kSlab, st.c[PAR ^ 1], c.lane);
   }
   const char* ks = st.k[PAR];
   const char* vs = st.v[PAR];
@@ -209,11 +266,11 @@ __device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, const 
   if (c.active) {
     f32x16 s1 = row_mfma<D>(c.q, ks, c.krow, 1);
     bf16x8 ds0[2], ds1[2];
-    ds_block(s0, dp0, c.delta, mk, 0, c.qframe, c.lane, ds0);
+    ds_block<false>(s0, dp0, c.delta, mk, nullptr, nullptr, false, 0, c.qframe, c.lane, ds0);
     const f32x16 dp1 = row_mfma<D>(c.dov, vs, c.krow, 1);
     p_exp(s1, c.c2, c.lse2);
     tr_mfma<D>(c.dq, ds0, ks, c.ktr, 0);
-    ds_block(s1, dp1, c.delta, mk, 1, c.qframe, c.lane, ds1);
+    ds_block<false>(s1, dp1, c.delta, mk, nullptr, nullptr, false, 1, c.qframe, c.lane, ds1);
     tr_mfma<D>(c.dq, ds1, ks, c.ktr, 1);
     // S(1) || dS(0); dP(1) || exp S(1); dQ(0) || dS(1); dQ(1)
     sched_phase<NC, 1, 7>();
@@ -225,12 +282,52 @@ __device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, const 
   __syncthreads();
 }
 
-template <int D>
+// A tile with a gated key (membership STE): the same copies and products, the
+// two 32-key blocks one after the other (fewer values live than in the
+// pipelined dq_tile, which leaves room for the per-class sums of dS).
+template <int D, int PAR>
+__device__ __forceinline__ void dq_tile_ste(QCtx<D>& c, int t, Idx<D>& inext,
+                                            const QStages& st) {
+  const bool more = t + 1 < c.nt;
+  if (more) {
+    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, st.k[PAR ^ 1], c.wave);
+    copy_dwords(c.kv_mask + (t + 1) * kSlab, st.m[PAR ^ 1], c.lane);
+    copy_dwords(c.kv_cls + (t + 1) * kSlab, st.c[PAR ^ 1], c.lane);
+  }
+  const char* ks = st.k[PAR];
+  const char* vs = st.v[PAR];
+  const uint32_t* mk = reinterpret_cast<const uint32_t*>(st.m[PAR]);
+  const uint32_t* cl = reinterpret_cast<const uint32_t*>(st.c[PAR]);
+  auto block = [&](int kb) {
+    f32x16 s = row_mfma<D>(c.q, ks, c.krow, kb);
+    const f32x16 dp = row_mfma<D>(c.dov, vs, c.krow, kb);
+    p_exp(s, c.c2, c.lse2);
+    bf16x8 ds[2];
+    ds_block<true>(s, dp, c.delta, mk, cl, c.ste, c.valid, kb, c.qframe, c.lane, ds);
+    tr_mfma<D>(c.dq, ds, ks, c.ktr, kb);
+  };
+  if (c.active) block(0);
+  if (more) {
+    copy_tile<D, kBothRead>(c.gv, c.v_ss_b, c.ck, inext, st.v[PAR ^ 1], c.wave);
+    inext = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+  }
+  if (c.active) block(1);
+  wait_copies();
+  __syncthreads();
+}
+
+// With STE (membership STE folded into this pass) the kernel also sums the
+// dS of each row's gated keys per class (tile_kv_class >= 0) into LDS slots
+// and writes them to ste_partial[h][row][class] for every row it owns.
+template <int D, bool STE>
 __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int total) {
+  constexpr int CB = STE ? Geo<D>::MBYTES : 16;
   __shared__ __align__(16) char lds_k0[Geo<D>::TILEB], lds_k1[Geo<D>::TILEB];
   __shared__ __align__(16) char lds_v0[Geo<D>::TILEB], lds_v1[Geo<D>::TILEB];
   __shared__ __align__(16) char lds_m0[Geo<D>::MBYTES], lds_m1[Geo<D>::MBYTES];
-  const QStages st = {{lds_k0, lds_k1}, {lds_v0, lds_v1}, {lds_m0, lds_m1}};
+  __shared__ __align__(16) char lds_c0[CB], lds_c1[CB];
+  __shared__ __align__(16) float lds_ste[STE ? kSteClasses * kSteSlots : 4];
+  const QStages st = {{lds_k0, lds_k1}, {lds_v0, lds_v1}, {lds_m0, lds_m1}, {lds_c0, lds_c1}};
   const int logical = hier::xcd_logical(blockIdx.x, gridDim.x);
   if (logical >= total) return;
   const int head = logical / a.n_items;
@@ -253,6 +350,8 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   c.v_ss_b = (uint32_t)(a.v_ss * 2);
   c.kv_idx = a.tile_kv_idx + kv_off;
   c.kv_mask = a.tile_kv_mask + kv_off;
+  c.kv_cls = STE ? a.tile_kv_class + kv_off : nullptr;
+  c.ste = lds_ste + (STE ? c.wave * 32 + (c.lane & 31) : 0);
   c.ck.init(c.wave, c.lane);
 #pragma unroll
   for (int i = 0; i < Geo<D>::NC; ++i) c.krow[i] = row_read_off<D, kBothRead>(c.lane, i);
@@ -294,25 +393,67 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   for (int db = 0; db < Geo<D>::NDB; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) c.dq[db][i] = 0.f;
+  if (STE && c.lane < 32)   // the lane's own slots (its partner lane adds after the first barrier)
+#pragma unroll
+    for (int cc = 0; cc < kSteClasses; ++cc) c.ste[cc * kSteSlots] = 0.f;
 
+  // With STE: does the tile in stage par hold a gated key?  Every wave reads
+  // the same LDS words, so every wave takes the same branch and meets the
+  // same barriers.
+  auto gated = [&](int par) {
+    const uint32_t w = reinterpret_cast<const uint32_t*>(st.c[par])[c.lane];
+    return __ballot(w < (uint32_t)kSteClasses) != 0;
+  };
   const int nt = c.nt;
   if (nt > 0) {
     const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
     copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, i0, st.k[0], c.wave);
     copy_tile<D, kBothRead>(c.gv, c.v_ss_b, c.ck, i0, st.v[0], c.wave);
     copy_dwords(c.kv_mask, st.m[0], c.lane);
+    if constexpr (STE) copy_dwords(c.kv_cls, st.c[0], c.lane);
     Idx<D> inext = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
     wait_copies();
     __syncthreads();
     int t = 0;
-    for (; t + 1 < nt; t += 2) {
-      dq_tile<D, 0>(c, t, inext, st);
-      dq_tile<D, 1>(c, t + 1, inext, st);
+    if constexpr (!STE) {
+      for (; t + 1 < nt; t += 2) {
+        dq_tile<D, 0, false>(c, t, inext, st);
+        dq_tile<D, 1, false>(c, t + 1, inext, st);
+      }
+      if (t < nt) dq_tile<D, 0, false>(c, t, inext, st);
+    } else {
+      // The pipelined tile up to the first tile with a gated key (a player
+      // row's gated keys, the local-hub keys, end its list), dq_tile_ste from
+      // there on.  Two loops rather than a choice per tile: with both
+      // variants in one loop body the registers no longer fit.  Tile t sits
+      // in stage t & 1.
+      bool stop = false;
+      for (; t + 1 < nt; t += 2) {
+        if (gated(0)) { stop = true; break; }
+        dq_tile<D, 0, true>(c, t, inext, st);
+        if (gated(1)) { ++t; stop = true; break; }
+        dq_tile<D, 1, true>(c, t + 1, inext, st);
+      }
+      if (!stop && t < nt && !gated(0)) dq_tile<D, 0, true>(c, t++, inext, st);
+      if (t < nt && (t & 1)) dq_tile_ste<D, 1>(c, t++, inext, st);
+      for (; t + 1 < nt; t += 2) {
+        dq_tile_ste<D, 0>(c, t, inext, st);
+        dq_tile_ste<D, 1>(c, t + 1, inext, st);
+      }
+      if (t < nt) dq_tile_ste<D, 0>(c, t, inext, st);
     }
-    if (t < nt) dq_tile<D, 0>(c, t, inext, st);
   }
   if (c.active && c.valid)
     store_acc<D>(a.dq + (int64_t)c.qtok * a.dq_ss + (int64_t)head * a.dq_sh, c.dq, a.scale, c.lane);
+  if constexpr (STE) {
+    // every tile ended with a barrier, so both lanes' adds are in the slots
+    if (c.valid && c.lane < 32) {
+      float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)c.qtok * kSteClasses;
+#pragma unroll
+      for (int cc = 0; cc < kSteClasses; ++cc)
+        if (cc < a.ste_classes) dst[cc] = c.ste[cc * kSteSlots];
+    }
+  }
 }
 
 // ---- dK, dV (key-major) ------------------------------------------------------
@@ -562,8 +703,6 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
 
 // ---- membership STE partial sums (query-major, gated keys only) -------------
 
-constexpr int kSteClasses = 16;
-
 // LDS: K[2] | V[2] (rows) | masks[2] | classes[2] | per-wave row sums
 template <int D>
 struct SLds {
@@ -574,26 +713,6 @@ struct SLds {
   static constexpr int AOFF = COFF + 2 * Geo<D>::MBYTES;
   static constexpr int SIZE = AOFF + kSteClasses * kWaves * 32 * 4;
 };
-
-// Adds a lane's 16 dS terms of one 32-key block into its class slots.  The
-// keys of a block mostly share one class (the lists keep each class's keys
-// together): a lane whose 16 keys do adds their sum once, otherwise each term.
-__device__ __forceinline__ void ste_add(float* acc, int slots, const float* ds,
-                                        const uint32_t* cls, bool valid) {
-  bool same = true;
-#pragma unroll
-  for (int i = 1; i < 16; ++i) same = same && cls[i] == cls[0];
-  if (!valid) return;
-  if (same) {
-    float t = ds[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) t += ds[i];
-    atomicAdd(&acc[cls[0] * slots], t);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) atomicAdd(&acc[cls[i] * slots], ds[i]);
-  }
-}
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int total) {
@@ -684,7 +803,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
           cls[i] = cl[e] & (kSteClasses - 1);
         }
       }
-      ste_add(acc, kSlots, ds, cls, valid);
+      ste_add(acc, ds, cls, valid);
     }
     __syncthreads();
     if (wave == 0 && valid && lane < 32) {
@@ -753,7 +872,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
             cls[i] = cl[e] & (kSteClasses - 1);
           }
         }
-        ste_add(acc, kSlots, ds, cls, valid);
+        ste_add(acc, ds, cls, valid);
       }
     }
     wait_copies();
@@ -809,15 +928,29 @@ int bwd_run(const HierBwdArgs& a, void* stream) {
     HIER_REQUIRE((int64_t)a.n_ste_items * a.H <= hier::kMaxLaunchItems, HIER_EUNSUPPORTED,
                  "too many work items");
   }
+  const bool fold = a.tile_kv_class != nullptr;
+  if (fold) {
+    HIER_REQUIRE(a.n_ste_items == 0, HIER_EINVAL,
+                 "membership STE: tile_kv_class (in the dQ pass) and an STE list are exclusive");
+    HIER_REQUIRE(a.ste_partial && al16(a.tile_kv_class), HIER_EINVAL,
+                 "membership STE: NULL ste_partial or misaligned tile_kv_class");
+    HIER_REQUIRE(a.ste_classes >= 1 && a.ste_classes <= kSteClasses, HIER_EUNSUPPORTED,
+                 "membership STE supports 1..%d classes (groups / players), got %d", kSteClasses,
+                 a.ste_classes);
+  }
   const int64_t tq = (int64_t)a.n_items * a.H, tk = (int64_t)a.n_key_items * a.H;
   HIER_REQUIRE(tq <= hier::kMaxLaunchItems && tk <= hier::kMaxLaunchItems, HIER_EUNSUPPORTED, "too many work items");
   hipStream_t s = (hipStream_t)stream;
   if (tq > 0) {
     const int grid = (int)hier::xcd_grid(tq);
-    if (a.D == 128)
-      hipLaunchKernelGGL(dq_kernel<128>, dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
+    if (a.D == 128 && fold)
+      hipLaunchKernelGGL((dq_kernel<128, true>), dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
+    else if (a.D == 128)
+      hipLaunchKernelGGL((dq_kernel<128, false>), dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
+    else if (fold)
+      hipLaunchKernelGGL((dq_kernel<64, true>), dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
     else
-      hipLaunchKernelGGL(dq_kernel<64>, dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
+      hipLaunchKernelGGL((dq_kernel<64, false>), dim3(grid), dim3(kThreads), 0, s, a, (int)tq);
     int rc = hier::check_launch("dq_kernel");
     if (rc != HIER_OK) return rc;
   }

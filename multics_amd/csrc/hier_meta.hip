@@ -873,17 +873,35 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_key_sizes_kernel(HierDe
   }
 }
 
-// STE selection of one entry of group d's list: class, or -1 if not kept.
-__device__ __forceinline__ int ste_class(const HierDeriveArgs& a, const GroupDesc& d, int k,
-                                         uint32_t m) {
+// STE selection of one entry (key k, mask m) of the list of the group whose
+// query rows start at token qbase: class, or -1 if not kept.
+__device__ __forceinline__ int ste_class_at(const HierDeriveArgs& a, int64_t qbase, int k,
+                                            uint32_t m) {
   const int64_t a0 = (int64_t)a.P * a.T * a.L, g0 = a0 + (int64_t)a.T * a.N * a.KL;
-  if (m == 0) return -1;
-  if (d.qbase < a0) {
+  if (m == 0 || k < 0 || qbase >= g0) return -1;
+  if (qbase < a0) {
     if (k < a0 || k >= g0) return -1;
     return (int)(((k - a0) / max(a.KL, 1)) % max(a.N, 1));
   }
   if (k >= a0) return -1;
   return (int)(k / ((int64_t)a.T * a.L));
+}
+
+__device__ __forceinline__ int ste_class(const HierDeriveArgs& a, const GroupDesc& d, int k,
+                                         uint32_t m) {
+  return ste_class_at(a, d.qbase, k, m);
+}
+
+// Class of every entry of the list of item i's group, written by the group's
+// first item (row_start 0); entries outside [0, kv_len) are never written.
+__global__ __launch_bounds__(kDeriveThreads) void derive_fwd_class_kernel(HierDeriveArgs a,
+                                                                         int32_t* cls) {
+  const int32_t* it = a.items + 8 * (int64_t)blockIdx.x;
+  if (it[3] != 0) return;
+  const int64_t qbase = it[0], off = it[5], cnt = it[6];
+  const int64_t lo = max(off, (int64_t)0), hi = min(off + cnt, (int64_t)a.kv_len);
+  for (int64_t e = lo + threadIdx.x; e < hi; e += blockDim.x)
+    cls[e] = ste_class_at(a, qbase, a.kv_idx[e], a.kv_mask[e]);
 }
 
 __device__ __forceinline__ bool ste_group(const HierDeriveArgs& a, const GroupDesc& d) {
@@ -1144,6 +1162,25 @@ extern "C" int hier_derive_count(const HierDeriveArgs* args, void* stream) {
   hipLaunchKernelGGL(derive_ste_count_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
   hipLaunchKernelGGL(derive_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a, w);
   return hier::check_launch("derive count kernels");
+}
+
+extern "C" int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class,
+                                       void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr && kv_class != nullptr, HIER_EINVAL, "NULL args or kv_class");
+  const HierDeriveArgs& a = *args;
+  HIER_REQUIRE(a.n_items >= 0 && a.kv_len >= 0, HIER_EINVAL, "invalid n_items=%d kv_len=%d",
+               a.n_items, a.kv_len);
+  HIER_REQUIRE(a.P >= 0 && a.T >= 0 && a.L >= 0 && a.N >= 0 && a.KL >= 0, HIER_EINVAL,
+               "invalid STE geometry");
+  HIER_REQUIRE(a.n_items == 0 || (a.items && a.kv_idx && a.kv_mask), HIER_EINVAL,
+               "NULL input pointer");
+  hipStream_t s = (hipStream_t)stream;
+  fill(kv_class, a.kv_len, -1, s);
+  if (a.n_items > 0)
+    hipLaunchKernelGGL(derive_fwd_class_kernel, dim3(a.n_items), dim3(kDeriveThreads), 0, s, a,
+                       kv_class);
+  return hier::check_launch("derive_fwd_class_kernel");
 }
 
 extern "C" int hier_derive_build(const HierDeriveArgs* args, void* stream) {

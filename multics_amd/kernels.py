@@ -17,7 +17,7 @@ import torch
 
 from . import _capi
 from . import metadata as M
-from .metadata import HierTiledBlockLayout, TileList, backward_lists
+from .metadata import HierTiledBlockLayout, TileList, backward_lists, ste_classes
 
 
 def _stream(dev) -> C.c_void_p:
@@ -94,6 +94,7 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
                             scale: Optional[float] = None,
                             key_tiles: Optional[TileList] = None,
                             ste_geometry: Optional[tuple] = None,
+                            ste_pass: str = "dq",
                             no_alloc_workspace: bool = False):
     """``hier_attn_bwd``: gradients ``(dq, dk, dv)`` (bf16, shaped like q/k/v) of
     ``hier_attention_forward(q, k, v, tiles)`` given its output, its ``lse``
@@ -102,7 +103,10 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
 
     With ``ste_geometry=(P, T, L, N, KL)`` a fourth result is returned: the
     sum of dS = P (dP - delta) over the membership-gated edges of every bit,
-    as an fp32 ``[T, N, P]`` tensor (see ``membership_grad``).
+    as an fp32 ``[T, N, P]`` tensor (see ``membership_grad``).  The sums are
+    taken inside the dQ pass over the forward list's gated entries
+    (``ste_pass="dq"``, the default) or by a separate pass over the STE list
+    (``ste_pass="list"``); both give the same sums up to fp32 rounding.
 
     ``no_alloc_workspace=True`` calls ``hier_attn_bwd_noalloc``, whose
     per-row workspace lives in the library's device array instead of a
@@ -131,16 +135,21 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     if lse.dtype != torch.float32 or lse.dim() != 2 or lse.shape[0] != H or \
             lse.shape[1] < tiles.row_extent or lse.stride(1) != 1:
         raise ValueError("lse must be fp32 [H, >=rows] with unit row stride")
-    ste = None
+    ste = cls = None
+    if ste_pass not in ("dq", "list"):
+        raise ValueError(f"ste_pass must be 'dq' or 'list', got {ste_pass!r}")
     if ste_geometry is not None:
         P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
         if max(P_, N_) > STE_CLASSES:
             raise NotImplementedError(f"membership STE supports up to {STE_CLASSES} players / groups")
-    if key_tiles is not None and ste_geometry is None:
+    list_ste = ste_geometry is not None and ste_pass == "list"
+    if key_tiles is not None and not list_ste:
         kt = key_tiles
     else:
-        kt, ste = backward_lists(tiles, ste_geometry)
+        kt, ste = backward_lists(tiles, ste_geometry if list_ste else None)
         kt = key_tiles if key_tiles is not None else kt
+    if ste_geometry is not None and not list_ste:
+        cls = ste_classes(tiles, ste_geometry)
     dev = q.device
     dq = torch.zeros_like(q3)
     dk = torch.zeros_like(k3)
@@ -169,6 +178,9 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         args.n_ste_items, args.ste_classes = sl.n_items, STE_CLASSES
         args.ste_items, args.ste_kv_idx = sl.items.data_ptr(), sl.kv_idx.data_ptr()
         args.ste_kv_mask, args.ste_kv_class = sl.kv_mask.data_ptr(), scls.data_ptr()
+        args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
+    if cls is not None:
+        args.ste_classes, args.tile_kv_class = STE_CLASSES, cls.data_ptr()
         args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
     _capi.call("hier_attn_bwd_noalloc" if no_alloc_workspace else "hier_attn_bwd", C.byref(args),
                _stream(dev))

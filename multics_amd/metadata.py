@@ -742,6 +742,56 @@ def ste_tiles_host(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int):
     return res
 
 
+def ste_classes_host(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int) -> np.ndarray:
+    """Membership-STE class of every entry of a full-sequence forward list
+    (``tile_kv_class`` of ``hier_attn_bwd``, which then sums the gated dS in
+    its dQ pass): the selection of ``ste_tiles_host`` kept in forward-list
+    order -- g for a local-hub key of group g in a player group's list, p for
+    a key of player p in a local-hub group's list, -1 for every other entry
+    and for entries with mask 0.  Host specification of the device builder
+    ``hier_derive_ste_classes`` (``ste_classes``); int32 ``[len(kv_idx)]``."""
+    a0, g0 = P * T * L, P * T * L + T * N * KL
+    items = tiles.items[:tiles.n_items].cpu().numpy().astype(np.int64)
+    kv_idx = tiles.kv_idx.cpu().numpy().astype(np.int64)
+    kv_mask = tiles.kv_mask.cpu().numpy().astype(np.int64) & 0xFFFFFFFF
+    cls = np.full(len(kv_idx), -1, np.int64)
+    for qb, off, cnt in items[items[:, 3] == 0][:, [0, 5, 6]]:
+        lo, hi = max(int(off), 0), min(int(off + cnt), len(kv_idx))
+        if qb >= g0 or hi <= lo:
+            continue
+        k, m = kv_idx[lo:hi], kv_mask[lo:hi]
+        if qb < a0:                      # player rows: local-hub keys, class = group
+            sel = (m != 0) & (k >= a0) & (k < g0)
+            c = ((k - a0) // max(KL, 1)) % max(N, 1)
+        else:                            # local-hub rows: player keys, class = player
+            sel = (m != 0) & (k >= 0) & (k < a0)
+            c = k // max(T * L, 1)
+        cls[lo:hi] = np.where(sel, c, -1)
+    return cls.astype(np.int32)
+
+
+def ste_classes(tiles: TileList, ste_geometry) -> torch.Tensor:
+    """``ste_classes_host`` of a device tile list, built on the GPU by
+    ``hier_derive_ste_classes`` and cached on ``tiles`` per geometry."""
+    key = tuple(int(x) for x in ste_geometry)
+    cache = tiles.__dict__.setdefault("_ste_classes", {})
+    hit = cache.get(key)
+    if hit is not None:
+        return hit
+    if not tiles.items.is_cuda:
+        raise NotImplementedError("ste_classes builds on the GPU; use ste_classes_host")
+    P, T, L, N, KL = key
+    n = int(tiles.kv_idx.numel())
+    a = _capi.HierDeriveArgs(n_items=tiles.n_items, kv_len=n, P=P, T=T, L=L, N=N, KL=KL,
+                             items=tiles.items.data_ptr(), kv_idx=tiles.kv_idx.data_ptr(),
+                             kv_mask=tiles.kv_mask.data_ptr())
+    cls = torch.empty(max(n, 4), dtype=torch.int32, device=tiles.items.device)
+    _capi.call("hier_derive_ste_classes", C.byref(a), cls.data_ptr(),
+               torch.cuda.current_stream(tiles.items.device).cuda_stream)
+    cache[key] = cls
+    return cls
+
+
 _DERIVE_ERRORS = ((1, "a token is a query row of two groups"),
                   (2, "a key is not a query row of any group"),
                   (4, "key lists are not whole key frames"),

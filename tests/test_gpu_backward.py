@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from multics_amd import metadata as M
-from multics_amd.kernels import hier_attention, hier_attention_backward
+from multics_amd.kernels import hier_attention, hier_attention_backward, hier_attention_forward
 from oracle.attention import masked_attention
 from oracle.masks import FullTopology
 from tests.gpu_util import need_gpu, say
@@ -161,3 +161,48 @@ def test_membership_ste_gradient_matches_oracle():
     _check("dv", vd.grad, vf.grad)
     _check("dlogits", lg.grad, lf.grad)
     assert (lf.grad != 0).any()
+
+
+@pytest.mark.parametrize("cfg", ["small", "c5"])
+def test_ste_in_dq_pass_equals_the_separate_pass(cfg):
+    """The membership STE summed inside the dQ pass (forward-list classes)
+    against the separate pass over the STE list: dQ / dK / dV bit-identical
+    (also to the backward without STE), the per-bit sums equal up to fp32
+    summation order."""
+    need_gpu()
+    import bench
+    if cfg == "c5":
+        P, T, L, N, KL, KG, n, W, _, D, grp = bench.CONFIGS["c5"]
+        logits, mem, go = bench.grouping(grp, P, T, N, np.random.default_rng(bench.SEED))
+        H = 4
+    else:
+        P, T, L, N, KL, KG, n, W, H, D = 4, 6, 24, 2, 5, 6, 3, 4, 2, 128
+        logits = np.random.default_rng(22).standard_normal((T, N, P)).astype(np.float32)
+        mem = logits > 0
+        go = ~mem.any(1)
+    topo = FullTopology(P, T, L, N, KL, KG, n, W, True, membership=mem, global_only=go)
+    full = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W, direct=True,
+                                    membership=mem, global_only=go)
+    tiles = M.build(full, "cuda").tiles
+    g = torch.Generator().manual_seed(5)
+    q, k, v = [(torch.randn(topo.S, H, D, generator=g) * 0.5).to(torch.bfloat16).cuda()
+               for _ in range(3)]
+    dout = torch.randn(topo.S, H, D, generator=g).to(torch.bfloat16).cuda()
+    say("STE in dQ vs separate pass", cfg, topo.S)
+    out = torch.zeros_like(q)
+    lse = torch.full((H, topo.S), float("-inf"), dtype=torch.float32, device="cuda")
+    hier_attention_forward(q, k, v, tiles, out, lse=lse)
+    geo = (P, T, L, N, KL)
+    plain = hier_attention_backward(q, k, v, out, dout, lse, tiles)
+    fold = hier_attention_backward(q, k, v, out, dout, lse, tiles, ste_geometry=geo)
+    sep = hier_attention_backward(q, k, v, out, dout, lse, tiles, ste_geometry=geo,
+                                  ste_pass="list")
+    torch.cuda.synchronize()
+    for i, name in enumerate(("dq", "dk", "dv")):
+        assert torch.equal(fold[i], plain[i]), name
+        assert torch.equal(sep[i], plain[i]), name
+    a, b = fold[3].double().cpu(), sep[3].double().cpu()
+    scale = b.abs().max().item()
+    say(f"  gated sums: max |fold - separate| {(a - b).abs().max().item():.3e} (max {scale:.3e})")
+    assert scale > 0 and (a != 0).any()
+    assert ((a - b).abs() <= 1e-5 * scale + 1e-6 * b.abs()).all()

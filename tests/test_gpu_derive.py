@@ -1,7 +1,9 @@
 """The backward's key-major and membership-STE lists built on the GPU
 (``hier_derive_count`` / ``hier_derive_build`` in csrc/hier_meta.hip) equal
 the host builders ``metadata.transpose_tiles_host`` / ``ste_tiles_host`` bit
-for bit: items, row / key indices, masks, per-64 ANDs, classes, pair count.
+for bit: items, row / key indices, masks, per-64 ANDs, classes, pair count;
+the STE classes of the forward list (``hier_derive_ste_classes``) equal
+``metadata.ste_classes_host``.
 
 Cases: every bench topology that has a full-sequence tile list (C2 fixed
 groups, P6 pairs, C3 per-frame dynamic groups, P10 random blocks, C5 soft
@@ -39,6 +41,10 @@ def _check_lists(tiles, geom):
     if geom is None:
         assert dev_ste is None
         return
+    host_cls = M.ste_classes_host(tiles, P=geom[0], T=geom[1], L=geom[2], N=geom[3], KL=geom[4])
+    dev_cls = M.ste_classes(tiles, geom)
+    _same(dev_cls[:len(host_cls)], torch.from_numpy(host_cls), "forward-list STE classes")
+    assert M.ste_classes(tiles, geom) is dev_cls                  # cached on the list
     host_ste = M.ste_tiles_host(tiles, P=geom[0], T=geom[1], L=geom[2], N=geom[3], KL=geom[4])
     assert (dev_ste is None) == (host_ste is None)
     if host_ste is None:
