@@ -179,9 +179,12 @@ int hier_derive_build(const HierDeriveArgs* args, void* stream);
 /* P..KL, items, kv_idx, kv_mask of args; no workspace, no pass 1): g for a */
 /* local-hub key of group g in a player group's list, p for a key of player */
 /* p in a local-hub group's list, -1 for every other entry and for masks of */
-/* 0 -- the selection of the STE list, kept in forward-list order.  Input   */
-/* tile_kv_class of hier_attn_bwd.                                          */
-int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class, void* stream);
+/* 0 -- the selection of the STE list, kept in forward-list order -- and    */
+/* item_first[i] = the first 64-entry tile of item i's list holding a class */
+/* (its tile count if none).  Inputs tile_kv_class / tile_ste_first of      */
+/* hier_attn_bwd.                                                           */
+int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class, int32_t* item_first,
+                            void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Q/K/V layout prologue: camera-pose Q/K adapter, RMSNorm over all heads,  */
@@ -299,10 +302,12 @@ typedef struct HierBwdArgs {
   int64_t ste_stride_h;            /* elements between heads of ste_partial    */
   /* Optional membership STE inside the dQ pass (instead of an STE list,    */
   /* n_ste_items must then be 0): the class of every entry of the forward    */
-  /* list (hier_derive_ste_classes; -1 or >= 16 = no gating bit).  The dQ    */
+  /* list (-1 or >= 16 = no gating bit) and per item the first 64-entry tile */
+  /* of its list with a class (both from hier_derive_ste_classes).  The dQ   */
   /* pass adds dS over each row's entries of class c into                    */
   /* ste_partial[h][row][c] and writes it for every row of every item.       */
   const int32_t* tile_kv_class;
+  const int32_t* tile_ste_first;   /* [n_items]                                */
 } HierBwdArgs;
 
 int hier_attn_bwd(const HierBwdArgs* args, void* stream);

@@ -86,7 +86,7 @@ class HierBwdArgs(C.Structure):
                [("n_ste_items", i32), ("ste_classes", i32)] + \
                [(n, vp) for n in ("ste_items", "ste_kv_idx", "ste_kv_mask", "ste_kv_class",
                                   "ste_partial")] + \
-               [("ste_stride_h", i64), ("tile_kv_class", vp)]
+               [("ste_stride_h", i64), ("tile_kv_class", vp), ("tile_ste_first", vp)]
 
 
 class HierPageArgs(C.Structure):
@@ -121,7 +121,7 @@ EXPORTS = {
     "hier_derive_workspace": [C.POINTER(HierDeriveArgs)],
     "hier_derive_count": [C.POINTER(HierDeriveArgs), vp],
     "hier_derive_build": [C.POINTER(HierDeriveArgs), vp],
-    "hier_derive_ste_classes": [C.POINTER(HierDeriveArgs), vp, vp],
+    "hier_derive_ste_classes": [C.POINTER(HierDeriveArgs), vp, vp, vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],

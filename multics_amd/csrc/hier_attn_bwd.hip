@@ -129,20 +129,6 @@ __device__ __forceinline__ void ste_add(float* acc, const float* ds, const uint3
   }
 }
 
-// The same for 4 keys (the dQ pass, whose registers are nearly all taken).
-__device__ __forceinline__ void ste_add4(float* acc, const float* ds, const u32x4& cls,
-                                         bool valid) {
-  const bool same = cls[1] == cls[0] && cls[2] == cls[0] && cls[3] == cls[0];
-  if (!valid) return;
-  if (same) {
-    if (cls[0] < kSteClasses) atomicAdd(&acc[cls[0] * kSteSlots], (ds[0] + ds[1]) + (ds[2] + ds[3]));
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (cls[e] < kSteClasses) atomicAdd(&acc[cls[e] * kSteSlots], ds[e]);
-  }
-}
-
 // ---- dQ (query-major) --------------------------------------------------------
 
 // LDS stages: K[2] (rows and transposed) | V[2] (rows) | masks[2] | STE
@@ -166,6 +152,7 @@ struct QCtx {
   const uint32_t* kv_mask;
   const int32_t* kv_cls;       // STE class of each list entry (membership STE only)
   float* ste;                  // the lane's row's STE slots, ste[class * kSteSlots]
+  int t1;                      // first tile with a gated key (membership STE only)
   uint32_t k_ss_b, v_ss_b;
   float c2;
   int nt, wave, lane;
@@ -211,19 +198,25 @@ template <bool STE>
 __device__ __forceinline__ void ds_block(const f32x16& p, const f32x16& dp, float delta,
                                          const uint32_t* mk, const uint32_t* cl, float* ste,
                                          bool valid, int kb, int qframe, int lane, bf16x8* dsb) {
+  float ds[16];
+  uint32_t cls[16];
 #pragma unroll
   for (int g4 = 0; g4 < 4; ++g4) {
     const int k0 = kb * 32 + 8 * g4 + 4 * (lane >> 5);
     const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[k0]);
-    float ds[4];
+    if constexpr (STE) {
+      const u32x4 c4 = *reinterpret_cast<const u32x4*>(&cl[k0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cls[4 * g4 + e] = c4[e];
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 4 * g4 + e;
-      ds[e] = __uint_as_float(__float_as_uint(p[i] * (dp[i] - delta)) & keep_mask(w[e], qframe));
-      dsb[i >> 3][i & 7] = (__bf16)ds[e];
+      ds[i] = __uint_as_float(__float_as_uint(p[i] * (dp[i] - delta)) & keep_mask(w[e], qframe));
+      dsb[i >> 3][i & 7] = (__bf16)ds[i];
     }
-    if constexpr (STE) ste_add4(ste, ds, *reinterpret_cast<const u32x4*>(&cl[k0]), valid);
   }
+  if constexpr (STE) ste_add(ste, ds, cls, valid);
 }
 
 // Tile t: works on stage PAR while tile t+1 is copied into stage PAR^1 in two
@@ -236,15 +229,15 @@ __device__ __forceinline__ void ds_block(const f32x16& p, const f32x16& dp, floa
 //     dP(1) || exp S(1) ; dQ(0) || dS(1) ; dQ(1)
 // (the masks are applied to every block: 16 ANDs under the MFMAs are cheaper
 // than a branch, which would split the schedule).
-// STE: the STE class words travel with the masks (the tile itself has no
-// gated key; dq_tile_ste handles those).
+// STE: a tile before the first one with a gated key (dq_tile_ste handles
+// those); the last such tile copies the class words of the next.
 template <int D, int PAR, bool STE>
 __device__ __forceinline__ void dq_tile(QCtx<D>& c, int t, Idx<D>& inext, const QStages& st) {
   const bool more = t + 1 < c.nt;
   if (more) {
     copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, st.k[PAR ^ 1], c.wave);
     copy_dwords(c.kv_mask + (t + 1) * kSlab, st.m[PAR ^ 1], c.lane);
-    if constexpr (STE) copy_dwords(c.kv_cls + (t + 1) * kSlab, st.c[PAR ^ 1], c.lane);
+    if (STE && t + 1 == c.t1) copy_dwords(c.kv_cls + (t + 1) * kSlab, st.c[PAR ^ 1], c.lane);
   }
   const char* ks = st.k[PAR];
   const char* vs = st.v[PAR];
@@ -351,6 +344,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   c.kv_idx = a.tile_kv_idx + kv_off;
   c.kv_mask = a.tile_kv_mask + kv_off;
   c.kv_cls = STE ? a.tile_kv_class + kv_off : nullptr;
+  c.t1 = STE ? min(max(a.tile_ste_first[item], 0), c.nt) : c.nt;
   c.ste = lds_ste + (STE ? c.wave * 32 + (c.lane & 31) : 0);
   c.ck.init(c.wave, c.lane);
 #pragma unroll
@@ -397,20 +391,13 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
 #pragma unroll
     for (int cc = 0; cc < kSteClasses; ++cc) c.ste[cc * kSteSlots] = 0.f;
 
-  // With STE: does the tile in stage par hold a gated key?  Every wave reads
-  // the same LDS words, so every wave takes the same branch and meets the
-  // same barriers.
-  auto gated = [&](int par) {
-    const uint32_t w = reinterpret_cast<const uint32_t*>(st.c[par])[c.lane];
-    return __ballot(w < (uint32_t)kSteClasses) != 0;
-  };
   const int nt = c.nt;
   if (nt > 0) {
     const Idx<D> i0 = load_idx<D>(c.kv_idx, 0, c.ck.idx_off);
     copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, i0, st.k[0], c.wave);
     copy_tile<D, kBothRead>(c.gv, c.v_ss_b, c.ck, i0, st.v[0], c.wave);
     copy_dwords(c.kv_mask, st.m[0], c.lane);
-    if constexpr (STE) copy_dwords(c.kv_cls, st.c[0], c.lane);
+    if (STE && c.t1 == 0) copy_dwords(c.kv_cls, st.c[0], c.lane);
     Idx<D> inext = load_idx<D>(c.kv_idx, min(1, nt - 1), c.ck.idx_off);
     wait_copies();
     __syncthreads();
@@ -422,19 +409,17 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
       }
       if (t < nt) dq_tile<D, 0, false>(c, t, inext, st);
     } else {
-      // The pipelined tile up to the first tile with a gated key (a player
-      // row's gated keys, the local-hub keys, end its list), dq_tile_ste from
-      // there on.  Two loops rather than a choice per tile: with both
-      // variants in one loop body the registers no longer fit.  Tile t sits
-      // in stage t & 1.
-      bool stop = false;
-      for (; t + 1 < nt; t += 2) {
-        if (gated(0)) { stop = true; break; }
+      // The pipelined tile up to the first tile with a gated key (t1, per
+      // item from the class builder; a player row's gated keys, the local-hub
+      // keys, end its list), dq_tile_ste from there on.  Two loops rather
+      // than a choice per tile: with both variants in one loop body the
+      // registers no longer fit.  Tile t sits in stage t & 1.
+      const int t1 = c.t1;
+      for (; t + 1 < t1; t += 2) {
         dq_tile<D, 0, true>(c, t, inext, st);
-        if (gated(1)) { ++t; stop = true; break; }
         dq_tile<D, 1, true>(c, t + 1, inext, st);
       }
-      if (!stop && t < nt && !gated(0)) dq_tile<D, 0, true>(c, t++, inext, st);
+      if (t < t1) dq_tile<D, 0, true>(c, t++, inext, st);
       if (t < nt && (t & 1)) dq_tile_ste<D, 1>(c, t++, inext, st);
       for (; t + 1 < nt; t += 2) {
         dq_tile_ste<D, 0>(c, t, inext, st);
@@ -932,8 +917,8 @@ int bwd_run(const HierBwdArgs& a, void* stream) {
   if (fold) {
     HIER_REQUIRE(a.n_ste_items == 0, HIER_EINVAL,
                  "membership STE: tile_kv_class (in the dQ pass) and an STE list are exclusive");
-    HIER_REQUIRE(a.ste_partial && al16(a.tile_kv_class), HIER_EINVAL,
-                 "membership STE: NULL ste_partial or misaligned tile_kv_class");
+    HIER_REQUIRE(a.ste_partial && a.tile_ste_first && al16(a.tile_kv_class), HIER_EINVAL,
+                 "membership STE: NULL ste_partial / tile_ste_first or misaligned tile_kv_class");
     HIER_REQUIRE(a.ste_classes >= 1 && a.ste_classes <= kSteClasses, HIER_EUNSUPPORTED,
                  "membership STE supports 1..%d classes (groups / players), got %d", kSteClasses,
                  a.ste_classes);

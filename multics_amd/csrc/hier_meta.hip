@@ -21,6 +21,7 @@
 #include "hier_common.h"
 
 #include <algorithm>
+#include <climits>
 
 namespace {
 
@@ -893,15 +894,29 @@ __device__ __forceinline__ int ste_class(const HierDeriveArgs& a, const GroupDes
 }
 
 // Class of every entry of the list of item i's group, written by the group's
-// first item (row_start 0); entries outside [0, kv_len) are never written.
+// first item (row_start 0; entries outside [0, kv_len) are never written),
+// and the first 64-entry tile of the list holding a class, for every item.
 __global__ __launch_bounds__(kDeriveThreads) void derive_fwd_class_kernel(HierDeriveArgs a,
-                                                                         int32_t* cls) {
+                                                                         int32_t* cls,
+                                                                         int32_t* first) {
+  __shared__ int s_first;
   const int32_t* it = a.items + 8 * (int64_t)blockIdx.x;
-  if (it[3] != 0) return;
   const int64_t qbase = it[0], off = it[5], cnt = it[6];
+  const bool writer = it[3] == 0;
+  if (threadIdx.x == 0) s_first = INT_MAX;
+  __syncthreads();
   const int64_t lo = max(off, (int64_t)0), hi = min(off + cnt, (int64_t)a.kv_len);
-  for (int64_t e = lo + threadIdx.x; e < hi; e += blockDim.x)
-    cls[e] = ste_class_at(a, qbase, a.kv_idx[e], a.kv_mask[e]);
+  int mine = INT_MAX;   // this thread's first entry with a class (its entries ascend)
+  for (int64_t e = lo + threadIdx.x; e < hi; e += blockDim.x) {
+    const int c = ste_class_at(a, qbase, a.kv_idx[e], a.kv_mask[e]);
+    if (writer) cls[e] = c;
+    if (c >= 0 && mine == INT_MAX) mine = (int)(e - off);
+  }
+  if (mine != INT_MAX) atomicMin(&s_first, mine);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    first[blockIdx.x] = s_first == INT_MAX ? (int)((max(cnt, (int64_t)0) + kTileKeys - 1) / kTileKeys)
+                                           : s_first / kTileKeys;
 }
 
 __device__ __forceinline__ bool ste_group(const HierDeriveArgs& a, const GroupDesc& d) {
@@ -1165,9 +1180,10 @@ extern "C" int hier_derive_count(const HierDeriveArgs* args, void* stream) {
 }
 
 extern "C" int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class,
-                                       void* stream) {
+                                       int32_t* item_first, void* stream) {
   hier::clear_error();
-  HIER_REQUIRE(args != nullptr && kv_class != nullptr, HIER_EINVAL, "NULL args or kv_class");
+  HIER_REQUIRE(args != nullptr && kv_class != nullptr && item_first != nullptr, HIER_EINVAL,
+               "NULL args, kv_class or item_first");
   const HierDeriveArgs& a = *args;
   HIER_REQUIRE(a.n_items >= 0 && a.kv_len >= 0, HIER_EINVAL, "invalid n_items=%d kv_len=%d",
                a.n_items, a.kv_len);
@@ -1179,7 +1195,7 @@ extern "C" int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_c
   fill(kv_class, a.kv_len, -1, s);
   if (a.n_items > 0)
     hipLaunchKernelGGL(derive_fwd_class_kernel, dim3(a.n_items), dim3(kDeriveThreads), 0, s, a,
-                       kv_class);
+                       kv_class, item_first);
   return hier::check_launch("derive_fwd_class_kernel");
 }
 

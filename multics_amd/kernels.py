@@ -180,7 +180,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         args.ste_kv_mask, args.ste_kv_class = sl.kv_mask.data_ptr(), scls.data_ptr()
         args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
     if cls is not None:
-        args.ste_classes, args.tile_kv_class = STE_CLASSES, cls.data_ptr()
+        args.ste_classes, args.tile_kv_class = STE_CLASSES, cls[0].data_ptr()
+        args.tile_ste_first = cls[1].data_ptr()
         args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
     _capi.call("hier_attn_bwd_noalloc" if no_alloc_workspace else "hier_attn_bwd", C.byref(args),
                _stream(dev))

@@ -770,9 +770,22 @@ def ste_classes_host(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int
     return cls.astype(np.int32)
 
 
-def ste_classes(tiles: TileList, ste_geometry) -> torch.Tensor:
-    """``ste_classes_host`` of a device tile list, built on the GPU by
-    ``hier_derive_ste_classes`` and cached on ``tiles`` per geometry."""
+def ste_first_tiles_host(tiles: TileList, cls: np.ndarray) -> np.ndarray:
+    """Per item, the first 64-entry tile of its list holding an STE class
+    (``tile_ste_first`` of ``hier_attn_bwd``; the list's tile count if none):
+    the dQ pass sums the STE from that tile on.  int32 ``[n_items]``."""
+    items = tiles.items[:tiles.n_items].cpu().numpy().astype(np.int64)
+    out = np.empty(len(items), np.int64)
+    for i, (off, cnt) in enumerate(items[:, [5, 6]]):
+        hit = np.nonzero(cls[max(off, 0):max(off + cnt, 0)] >= 0)[0]
+        out[i] = hit[0] // TILE_KEYS if len(hit) else -(-cnt // TILE_KEYS)
+    return out.astype(np.int32)
+
+
+def ste_classes(tiles: TileList, ste_geometry):
+    """``(ste_classes_host, ste_first_tiles_host)`` of a device tile list as
+    device tensors, built on the GPU by ``hier_derive_ste_classes`` and cached
+    on ``tiles`` per geometry."""
     key = tuple(int(x) for x in ste_geometry)
     cache = tiles.__dict__.setdefault("_ste_classes", {})
     hit = cache.get(key)
@@ -786,10 +799,11 @@ def ste_classes(tiles: TileList, ste_geometry) -> torch.Tensor:
                              items=tiles.items.data_ptr(), kv_idx=tiles.kv_idx.data_ptr(),
                              kv_mask=tiles.kv_mask.data_ptr())
     cls = torch.empty(max(n, 4), dtype=torch.int32, device=tiles.items.device)
-    _capi.call("hier_derive_ste_classes", C.byref(a), cls.data_ptr(),
+    first = torch.empty(max(tiles.n_items, 1), dtype=torch.int32, device=tiles.items.device)
+    _capi.call("hier_derive_ste_classes", C.byref(a), cls.data_ptr(), first.data_ptr(),
                torch.cuda.current_stream(tiles.items.device).cuda_stream)
-    cache[key] = cls
-    return cls
+    cache[key] = (cls, first)
+    return cache[key]
 
 
 _DERIVE_ERRORS = ((1, "a token is a query row of two groups"),

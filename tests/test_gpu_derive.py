@@ -42,9 +42,11 @@ def _check_lists(tiles, geom):
         assert dev_ste is None
         return
     host_cls = M.ste_classes_host(tiles, P=geom[0], T=geom[1], L=geom[2], N=geom[3], KL=geom[4])
-    dev_cls = M.ste_classes(tiles, geom)
+    dev_cls, dev_first = M.ste_classes(tiles, geom)
     _same(dev_cls[:len(host_cls)], torch.from_numpy(host_cls), "forward-list STE classes")
-    assert M.ste_classes(tiles, geom) is dev_cls                  # cached on the list
+    _same(dev_first[:tiles.n_items], torch.from_numpy(M.ste_first_tiles_host(tiles, host_cls)),
+          "first tile with a class")
+    assert M.ste_classes(tiles, geom)[0] is dev_cls               # cached on the list
     host_ste = M.ste_tiles_host(tiles, P=geom[0], T=geom[1], L=geom[2], N=geom[3], KL=geom[4])
     assert (dev_ste is None) == (host_ste is None)
     if host_ste is None:

@@ -100,3 +100,19 @@ def test_classes_select_the_ste_list(kind):
         np.testing.assert_array_equal(kv_mask[sel][order], smask[so:so + sn])
         np.testing.assert_array_equal(cls[sel][order], scls[so:so + sn])
         assert (smask[so + sn:so + int(srow[6])] == 0).all()       # the rest is padding
+
+
+@pytest.mark.parametrize("kind", ["membership", "dense_unbounded", "labels"])
+def test_first_tile_with_a_class(kind):
+    topo = _topology(kind)
+    tiles = synth_forward_tiles(topo)
+    cls = M.ste_classes_host(tiles, P=topo.P, T=topo.T, L=topo.L, N=topo.N, KL=topo.KL)
+    first = M.ste_first_tiles_host(tiles, cls)
+    items = tiles.items.numpy().astype(np.int64)
+    assert first.dtype == np.int32 and len(first) == len(items)
+    for f, (off, cnt) in zip(first, items[:, [5, 6]]):
+        tiles_cls = cls[off:off + cnt].reshape(-1, 64)
+        has = (tiles_cls >= 0).any(1)
+        assert not has[:f].any()
+        assert f == len(has) or has[f]
+    assert (first < items[:, 6] // 64).any() and (first == items[:, 6] // 64).any()
