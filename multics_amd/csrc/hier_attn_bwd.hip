@@ -4,7 +4,7 @@
 // delta = rowsum(dO * O) and dS = P * (dP - delta):
 //   dQ = scale * dS K,   dK = scale * dS^T Q,   dV = P^T dO.
 // Two kernels, each writing every gradient row from exactly one workgroup
-// (deterministic, no atomics):
+// (deterministic, no global atomics):
 //
 // dq_kernel   query-major, over the forward tile list (128 query rows per
 //             item, 4 waves x 32).  Per 32-key block:
@@ -28,6 +28,10 @@
 // permuted k order of the next MFMA's register operand, so P and dS go from
 // the accumulators to bf16 operands without any shuffle.  Tiles are copied
 // with global_load_lds_dwordx4 into the swizzled layouts of hier_tile.h.
+//
+// Membership STE: with tile_kv_class set, dq_kernel also sums the fp32 dS
+// of each row's membership-gated keys per class (dq_kernel<D, true>);
+// ste_kernel does the same over a separate list of the gated keys only.
 #include "hier_common.h"
 #include "hier_launch.h"
 #include "hier_tile.h"
