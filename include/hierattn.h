@@ -290,15 +290,16 @@ typedef struct HierBwdArgs {
   /* local-hub rows of group g, both at the query frame -- with per key the  */
   /* class c (g for player rows, p for local-hub rows).  The pass adds      */
   /* dS = P (dP - delta) over each row's keys of class c into                */
-  /* ste_partial[h][row][c] (fp32, c < ste_classes <= 16, zero-initialised */
-  /* by the caller); rows of other items are untouched.                     */
+  /* ste_partial[h][row][c] (fp32, row stride ste_classes <= 16: classes    */
+  /* >= ste_classes are dropped; zero-initialised by the caller); rows of    */
+  /* other items are untouched.                                              */
   int32_t n_ste_items;
   int32_t ste_classes;
   const int32_t* ste_items;
   const int32_t* ste_kv_idx;
   const uint32_t* ste_kv_mask;
   const int32_t* ste_kv_class;
-  float* ste_partial;              /* [H][ste_rows][16]                        */
+  float* ste_partial;              /* [H][ste_rows][ste_classes]               */
   int64_t ste_stride_h;            /* elements between heads of ste_partial    */
   /* Optional membership STE inside the dQ pass (instead of an STE list,    */
   /* n_ste_items must then be 0): the class of every entry of the forward    */

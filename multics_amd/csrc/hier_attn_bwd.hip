@@ -437,7 +437,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   if constexpr (STE) {
     // every tile ended with a barrier, so both lanes' adds are in the slots
     if (c.valid && c.lane < 32) {
-      float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)c.qtok * kSteClasses;
+      float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)c.qtok * a.ste_classes;
 #pragma unroll
       for (int cc = 0; cc < kSteClasses; ++cc)
         if (cc < a.ste_classes) dst[cc] = c.ste[cc * kSteSlots];
@@ -797,7 +797,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
     __syncthreads();
     if (wave == 0 && valid && lane < 32) {
       const float* sum = reinterpret_cast<const float*>(lds + SLds<D>::AOFF) + lane;
-      float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)qtok * kSteClasses;
+      float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)qtok * a.ste_classes;
 #pragma unroll
       for (int cc = 0; cc < kSteClasses; ++cc)
         if (cc < a.ste_classes) {
@@ -868,7 +868,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
     __syncthreads();
   }
   if (active && valid && lane < 32) {
-    float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)qtok * kSteClasses;
+    float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)qtok * a.ste_classes;
 #pragma unroll
     for (int cc = 0; cc < kSteClasses; ++cc)
       if (cc < a.ste_classes) dst[cc] = acc[cc * kSlots];

@@ -157,7 +157,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     ws = None if no_alloc_workspace else \
         torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
     if ste_geometry is not None:
-        partial = torch.zeros((H, tiles.row_extent, STE_CLASSES), dtype=torch.float32, device=dev)
+        n_cls = max(P_, N_)     # classes are groups (player rows) or players (hub rows)
+        partial = torch.zeros((H, tiles.row_extent, n_cls), dtype=torch.float32, device=dev)
     args = _capi.HierBwdArgs(
         H=H, D=D, n_items=tiles.n_items, n_key_items=kt.n_items,
         scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
@@ -175,12 +176,12 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         key_q_mask=kt.kv_mask.data_ptr(), key_blk_and=kt.blk_and.data_ptr())
     if ste is not None:
         sl, scls = ste
-        args.n_ste_items, args.ste_classes = sl.n_items, STE_CLASSES
+        args.n_ste_items, args.ste_classes = sl.n_items, n_cls
         args.ste_items, args.ste_kv_idx = sl.items.data_ptr(), sl.kv_idx.data_ptr()
         args.ste_kv_mask, args.ste_kv_class = sl.kv_mask.data_ptr(), scls.data_ptr()
         args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
     if cls is not None:
-        args.ste_classes, args.tile_kv_class = STE_CLASSES, cls[0].data_ptr()
+        args.ste_classes, args.tile_kv_class = n_cls, cls[0].data_ptr()
         args.tile_ste_first = cls[1].data_ptr()
         args.ste_partial, args.ste_stride_h = partial.data_ptr(), partial.stride(0)
     _capi.call("hier_attn_bwd_noalloc" if no_alloc_workspace else "hier_attn_bwd", C.byref(args),
@@ -191,8 +192,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         return res
     P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
     a0 = P_ * T_ * L_
-    g_player = partial[:, :a0].reshape(H, P_, T_, L_, STE_CLASSES).sum(dim=(0, 3))[..., :N_]
-    g_local = partial[:, a0:a0 + T_ * N_ * KL_].reshape(H, T_, N_, KL_, STE_CLASSES)
+    g_player = partial[:, :a0].reshape(H, P_, T_, L_, n_cls).sum(dim=(0, 3))[..., :N_]
+    g_local = partial[:, a0:a0 + T_ * N_ * KL_].reshape(H, T_, N_, KL_, n_cls)
     g_local = g_local.sum(dim=(0, 3))[..., :P_]
     return res + (g_player.permute(1, 2, 0) + g_local,)
 
