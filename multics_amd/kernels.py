@@ -89,6 +89,20 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
 STE_CLASSES = 16
 
 
+def _covers_all_rows(tiles: TileList) -> bool:
+    """Whether the items of a full-sequence list own every row once: their row
+    counts sum to the row extent (the list builders give each token to one
+    (block, stream) group and split a group's rows between its items), and
+    queries and keys are the same rows.  Then dq_kernel writes every row of
+    dQ and dkv_kernel every row of dK / dV.  Cached on the list."""
+    hit = tiles.__dict__.get("_covers_rows")
+    if hit is None:
+        rows = tiles.items[:tiles.n_items, 4].to(torch.int64).sum().item() if tiles.n_items else 0
+        hit = tiles.row_extent == tiles.key_extent and rows == tiles.row_extent
+        tiles.__dict__["_covers_rows"] = hit
+    return hit
+
+
 def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                             dout: torch.Tensor, lse: torch.Tensor, tiles: TileList, *,
                             scale: Optional[float] = None,
@@ -151,9 +165,14 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     if ste_geometry is not None and not list_ste:
         cls = ste_classes(tiles, ste_geometry)
     dev = q.device
-    dq = torch.zeros_like(q3)
-    dk = torch.zeros_like(k3)
-    dv = torch.zeros_like(v3)
+    # every row the kernels own is written; the buffers need clearing only
+    # when some row of q / k / v belongs to no work item
+    full = _covers_all_rows(tiles) and q3.shape[0] == tiles.row_extent and \
+        k3.shape[0] == tiles.key_extent and v3.shape[0] == tiles.key_extent
+    alloc = torch.empty_like if full else torch.zeros_like
+    dq = alloc(q3)
+    dk = alloc(k3)
+    dv = alloc(v3)
     ws = None if no_alloc_workspace else \
         torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
     if ste_geometry is not None:

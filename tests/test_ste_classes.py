@@ -116,3 +116,4 @@ def test_first_tile_with_a_class(kind):
         assert not has[:f].any()
         assert f == len(has) or has[f]
     assert (first < items[:, 6] // 64).any() and (first == items[:, 6] // 64).any()
+

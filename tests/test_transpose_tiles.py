@@ -134,3 +134,17 @@ def test_transpose_rejects_partial_frames():
                      key_extent=fwd.key_extent, row_extent=fwd.row_extent)
     with pytest.raises(AssertionError):
         M.transpose_tiles(bad)
+
+
+def test_row_coverage_decides_whether_gradients_are_cleared():
+    """The backward leaves dQ / dK / dV uncleared only when its items own
+    every row once (``kernels._covers_all_rows``)."""
+    import dataclasses
+    from multics_amd.kernels import _covers_all_rows
+    rng = np.random.default_rng(3)
+    mem = rng.random((6, 2, 4)) < 0.4
+    tiles = synth_forward_tiles(FullTopology(4, 6, 3, 2, 2, 2, 3, 4, True, membership=mem,
+                                             global_only=~mem.any(1)))
+    assert _covers_all_rows(tiles)
+    fewer = dataclasses.replace(tiles, n_items=tiles.n_items - 1)
+    assert not _covers_all_rows(fewer)
