@@ -247,8 +247,14 @@ class HierAttentionFunction(torch.autograd.Function):
                 logits: Optional[torch.Tensor] = None, ste_geometry: Optional[tuple] = None):
         q3 = _rows_view(q)[0]
         H = q3.shape[1]
-        out = torch.zeros_like(q)
-        lse = torch.full((H, q3.shape[0]), float("-inf"), dtype=torch.float32, device=q.device)
+        if _covers_all_rows(tiles) and q3.shape[0] == tiles.row_extent:
+            # the kernel writes every row's output and LSE (0 and -inf for a
+            # row that sees no key)
+            out = torch.empty_like(q)
+            lse = torch.empty((H, q3.shape[0]), dtype=torch.float32, device=q.device)
+        else:
+            out = torch.zeros_like(q)
+            lse = torch.full((H, q3.shape[0]), float("-inf"), dtype=torch.float32, device=q.device)
         hier_attention_forward(q, k, v, tiles, out, lse=lse, scale=scale)
         if logits is not None:
             ctx.save_for_backward(q, k, v, out, lse, logits)

@@ -34,7 +34,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import metadata as M
-from .kernels import hier_attention, hier_attention_forward, qkv_prologue
+from .kernels import _covers_all_rows, hier_attention, hier_attention_forward, qkv_prologue
 from .hier_masks import HierBlockMask
 from .kv_cache import stream_pool
 from .paged_cache import HierPagedKVCache
@@ -78,6 +78,15 @@ def rope_apply(x: torch.Tensor, freqs: torch.Tensor, num_heads: int) -> torch.Te
     b, s, dim = x.shape
     xc = torch.view_as_complex(x.to(torch.float64).reshape(b, s, num_heads, -1, 2))
     return torch.view_as_real(xc * freqs.to(x.device)).flatten(2).to(x.dtype)
+
+
+def _attn_out(tiles, s, H, D, device):
+    """Output buffer of a full-sequence forward: uncleared when the list's
+    items own every one of the s rows (the kernel then writes each, 0 for a
+    row that sees no key), zero-filled otherwise."""
+    if _covers_all_rows(tiles) and tiles.row_extent == s:
+        return torch.empty((s, H, D), dtype=torch.bfloat16, device=device)
+    return torch.zeros((s, H, D), dtype=torch.bfloat16, device=device)
 
 
 class SelfAttention(nn.Module):
@@ -195,7 +204,7 @@ class SelfAttention(nn.Module):
                                ste_geometry=geometry)
         else:
             q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
-            y = torch.zeros((s, H, D), dtype=torch.bfloat16, device=x.device)
+            y = _attn_out(tiles, s, H, D, x.device)
             hier_attention_forward(q, k, v, tiles, y)
         return self.o(y.reshape(1, s, dim).to(self.o.weight.dtype))
 
@@ -286,7 +295,7 @@ class SelfAttention(nn.Module):
             y = hier_attention(q, k, v, mask.tiles)
         else:
             q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
-            y = torch.zeros((s, H, D), dtype=torch.bfloat16, device=x.device)
+            y = _attn_out(mask.tiles, s, H, D, x.device)
             hier_attention_forward(q, k, v, mask.tiles, y)
         if mask.self_rows.numel():
             rows = mask.self_rows.to(x.device)
