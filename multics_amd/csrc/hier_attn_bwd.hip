@@ -789,7 +789,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
           const int i = 4 * g4 + e;
           const float p = __builtin_amdgcn_exp2f(fmaf(s[i], c2, -lse2));
           ds[i] = __uint_as_float(__float_as_uint(p * (dp[i] - delta)) & keep_mask(w[e], qframe));
-          cls[i] = cl[e] & (kSteClasses - 1);
+          cls[i] = cl[e];   // >= kSteClasses (or -1): dropped by ste_add
         }
       }
       ste_add(acc, ds, cls, valid);
@@ -858,7 +858,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
             const int i = 4 * g4 + e;
             const float p = __builtin_amdgcn_exp2f(fmaf(s[i], c2, -lse2));
             ds[i] = __uint_as_float(__float_as_uint(p * (dp[i] - delta)) & keep_mask(w[e], qframe));
-            cls[i] = cl[e] & (kSteClasses - 1);
+            cls[i] = cl[e];   // >= kSteClasses (or -1): dropped by ste_add
           }
         }
         ste_add(acc, ds, cls, valid);
@@ -875,9 +875,6 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
   }
 }
 
-int64_t span_bytes(int64_t rows, int64_t ss, int64_t sh, int H, int D) {
-  return ((rows > 0 ? rows - 1 : 0) * ss + (int64_t)(H - 1) * sh + D) * 2;
-}
 
 // Argument checks and the launches of both entry points (a is complete: the
 // workspace pointers are set).
@@ -897,10 +894,11 @@ int bwd_run(const HierBwdArgs& a, void* stream) {
                         a.do_ss, a.do_sh, a.dq_ss, a.dq_sh, a.dk_ss, a.dk_sh, a.dv_ss, a.dv_sh};
   for (int64_t s : st)
     HIER_REQUIRE(s >= 0 && s % 8 == 0, HIER_EINVAL, "strides must be non-negative multiples of 8");
-  HIER_REQUIRE(span_bytes(a.kv_rows, a.k_ss, a.k_sh, a.H, a.D) <= (1ll << 32) &&
-                   span_bytes(a.kv_rows, a.v_ss, a.v_sh, a.H, a.D) <= (1ll << 32) &&
-                   span_bytes(a.q_rows, a.q_ss, a.q_sh, a.H, a.D) <= (1ll << 32) &&
-                   span_bytes(a.q_rows, a.do_ss, a.do_sh, a.H, a.D) <= (1ll << 32),
+  constexpr __int128 k4G = (__int128)1 << 32;
+  HIER_REQUIRE(hier::span_bytes(a.kv_rows, a.k_ss, a.k_sh, a.H, a.D) <= k4G &&
+                   hier::span_bytes(a.kv_rows, a.v_ss, a.v_sh, a.H, a.D) <= k4G &&
+                   hier::span_bytes(a.q_rows, a.q_ss, a.q_sh, a.H, a.D) <= k4G &&
+                   hier::span_bytes(a.q_rows, a.do_ss, a.do_sh, a.H, a.D) <= k4G,
                HIER_EUNSUPPORTED, "Q/K/V/dO views must span at most 4 GiB");
   HIER_REQUIRE(copy_rows_ok(a.kv_rows, a.k_ss) && copy_rows_ok(a.kv_rows, a.v_ss) &&
                    copy_rows_ok(a.q_rows, a.q_ss) && copy_rows_ok(a.q_rows, a.do_ss),
@@ -1022,6 +1020,11 @@ extern "C" int hier_attn_bwd_noalloc(const HierBwdArgs* args, void* stream) {
                "be NULL");
   HIER_REQUIRE(args->H >= 1 && args->lse_stride_h >= 0, HIER_EINVAL,
                "invalid H=%d lse_stride_h=%lld", args->H, (long long)args->lse_stride_h);
+  HIER_REQUIRE(args->H <= kScratchFloats && args->lse_stride_h <= kScratchFloats,
+               HIER_EUNSUPPORTED,
+               "hier_attn_bwd_noalloc workspace holds 2 x H x lse_stride_h <= %lld floats; got "
+               "H=%d x lse_stride_h=%lld",
+               (long long)kScratchFloats, args->H, (long long)args->lse_stride_h);
   // delta and lse2 each take H rows of lse_stride_h floats, rounded to 64
   // floats so that lse2 starts 256-byte aligned
   const int64_t per = ((int64_t)args->H * args->lse_stride_h + 63) / 64 * 64;

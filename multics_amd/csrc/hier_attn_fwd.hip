@@ -605,12 +605,10 @@ extern "C" int hier_attn_fwd(const HierFwdArgs* args, void* stream) {
   HIER_REQUIRE(a.k_ss >= 0 && a.k_sh >= 0 && a.v_ss >= 0 && a.v_sh >= 0, HIER_EINVAL,
                "K/V strides must be non-negative");
   // K / V rows are addressed with 32-bit byte offsets from k / v.
-  const int64_t rows = a.kv_rows > 0 ? a.kv_rows - 1 : 0;
-  const int64_t k_ext = (rows * a.k_ss + (int64_t)(a.H - 1) * a.k_sh + a.D) * 2;
-  const int64_t v_ext = (rows * a.v_ss + (int64_t)(a.H - 1) * a.v_sh + a.D) * 2;
-  HIER_REQUIRE(k_ext <= (1ll << 32) && v_ext <= (1ll << 32), HIER_EUNSUPPORTED,
-               "K/V views must span at most 4 GiB (got %lld / %lld bytes)", (long long)k_ext,
-               (long long)v_ext);
+  const __int128 k_ext = hier::span_bytes(a.kv_rows, a.k_ss, a.k_sh, a.H, a.D);
+  const __int128 v_ext = hier::span_bytes(a.kv_rows, a.v_ss, a.v_sh, a.H, a.D);
+  HIER_REQUIRE(k_ext <= ((__int128)1 << 32) && v_ext <= ((__int128)1 << 32), HIER_EUNSUPPORTED,
+               "K/V views must span at most 4 GiB");
   HIER_REQUIRE(copy_rows_ok(a.kv_rows, a.k_ss) && copy_rows_ok(a.kv_rows, a.v_ss),
                HIER_EUNSUPPORTED, "K/V need at most 2^24 rows and a row stride under 8M elements");
   if (a.n_items == 0) return HIER_OK;

@@ -25,6 +25,14 @@ inline int fail(int code, const char* fmt, ...) {
 
 inline void clear_error() { g_last_error[0] = 0; }
 
+// Bytes spanned by a [rows][H][D] bf16 view with element strides ss and sh:
+// ((rows - 1) * ss + (H - 1) * sh + D) * 2, in 128-bit arithmetic so that no
+// caller-given stride can overflow it.  Strides must be non-negative.
+inline __int128 span_bytes(int64_t rows, int64_t ss, int64_t sh, int64_t H, int64_t D) {
+  const __int128 r = rows > 0 ? rows - 1 : 0, h = H > 0 ? H - 1 : 0;
+  return (r * ss + h * sh + D) * 2;
+}
+
 inline int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(HIER_ELAUNCH, "%s: %s", what, hipGetErrorString(e));

@@ -550,6 +550,18 @@ int validate(const HierTopo* t) {
                "n_frames must be in [1,32], got %d", t->n_frames);
   HIER_REQUIRE(t->n_block >= 1, HIER_EINVAL, "n_block must be >= 1");
   HIER_REQUIRE(t->B >= 1, HIER_EINVAL, "B must be >= 1");
+  HIER_REQUIRE(t->fa_max >= 0 && t->fl_max >= 0 && t->fg_max >= 0, HIER_EINVAL,
+               "invalid frame pitches fa_max=%d fl_max=%d fg_max=%d", t->fa_max, t->fl_max,
+               t->fg_max);
+  // bounds that keep every size product below in 64 bits (the run bound
+  // below implies P, N, fa_max, fl_max, fg_max <= kMaxRuns + 1 anyway)
+  HIER_REQUIRE(t->P <= kMaxRuns + 1 && t->N <= kMaxRuns + 1 && t->fa_max <= kMaxRuns &&
+                   t->fl_max <= kMaxRuns && t->fg_max <= kMaxRuns && t->L <= (1 << 20) &&
+                   t->KL <= (1 << 20) && t->KG <= (1 << 20) && t->B <= (1 << 20),
+               HIER_EUNSUPPORTED, "topology too large (P=%d N=%d L=%d B=%d)", t->P, t->N, t->L,
+               t->B);
+  HIER_REQUIRE((int64_t)t->B * (t->P + t->N + 1) <= INT32_MAX, HIER_EUNSUPPORTED,
+               "too many (block, stream) groups");
   HIER_REQUIRE(!t->no_local || t->KL == 0, HIER_EINVAL, "no_local requires K_L=0");
   HIER_REQUIRE(t->fa && t->fl && t->fg && t->agent_frames && t->global_frames && t->q_frames &&
                    t->q_active && t->ref_agent_base && t->ref_global_base &&
@@ -693,6 +705,14 @@ __host__ __device__ inline int64_t derive_ws_layout(const HierDeriveArgs& a, Der
   d.s_item_off = reinterpret_cast<int64_t*>(take(8 * (ng + 1)));
   if (w) *w = d;
   return o;
+}
+
+// Sizes the workspace layout accepts: non-negative, at most 32 frames per
+// group and a table of at most kMaxTable entries (n_groups <= 8192), so every
+// byte count of the layout fits in 64 bits.
+inline bool derive_sizes_ok(const HierDeriveArgs& a) {
+  return a.n_items >= 0 && a.n_groups >= 0 && a.rows >= 0 && a.nq_max >= 0 && a.nq_max <= 32 &&
+         (int64_t)a.n_groups * a.n_groups <= kMaxTable;
 }
 
 __device__ __forceinline__ void flag(int64_t* totals, int e) {
@@ -986,9 +1006,12 @@ __global__ __launch_bounds__(kScanThreads) void derive_key_write_kernel(HierDeri
   __shared__ int64_t sh[kScanThreads];
   __shared__ int32_t u_off[kScanThreads];
   __shared__ int32_t u_id[kScanThreads];
+  // after a flagged pass 1 the offsets are not trusted: nothing is written
+  if (a.totals[4] != 0) return;
   const int G = blockIdx.x;
   const int ng = a.n_groups, nq = a.nq_max, nu = ng * nq;
   const int64_t base = w.t_off[G];
+  const int64_t lim = a.key_entries;   // the caller's list size bounds every store
   const int padded = w.t_size[G];
   const uint32_t* row = w.table + (int64_t)G * nu;
   int64_t done = 0;   // entries written before this chunk of units
@@ -1016,13 +1039,16 @@ __global__ __launch_bounds__(kScanThreads) void derive_key_write_kernel(HierDeri
       const int uu = u_id[lo], gg = uu / nq, j = uu - gg * nq;
       const GroupDesc q = group_desc(a, w, gg);
       const int r = p - u_off[lo];
-      a.key_q_idx[base + done + p] = q.qbase + j * q.qstride + r;
-      a.key_q_mask[base + done + p] = row[uu];
+      const int64_t o = base + done + p;
+      if (o < lim) {
+        a.key_q_idx[o] = q.qbase + j * q.qstride + r;
+        a.key_q_mask[o] = row[uu];
+      }
     }
     done += chunk;
     __syncthreads();
   }
-  for (int64_t p = done + threadIdx.x; p < padded; p += blockDim.x) {
+  for (int64_t p = done + threadIdx.x; p < padded && base + p < lim; p += blockDim.x) {
     a.key_q_idx[base + p] = 0;
     a.key_q_mask[base + p] = 0;
   }
@@ -1035,12 +1061,14 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_ste_write_kernel(HierDe
                                                                          DeriveWs w) {
   __shared__ int cbase[kClasses];     // first position of each class in the list
   __shared__ int wcnt[kDeriveThreads / 64][kClasses];
+  if (a.totals[4] != 0) return;       // flagged pass 1: nothing is written
   const int g = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const GroupDesc d = group_desc(a, w, g);
   const int padded = w.s_size[g];
   if (padded == 0) return;
   const int64_t base = w.s_off[g];
+  const int64_t lim = a.ste_entries, item_lim = a.totals[3];
   if (threadIdx.x == 0) {
     int acc = 0;
     for (int c = 0; c < kClasses; ++c) {
@@ -1076,9 +1104,11 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_ste_write_kernel(HierDe
       int before = 0;
       for (int v = 0; v < wave; ++v) before += wcnt[v][c];
       const int64_t pos = base + cbase[c] + before + rank;
-      a.ste_kv_idx[pos] = k;
-      a.ste_kv_mask[pos] = m;
-      a.ste_kv_class[pos] = c;
+      if (pos < lim) {
+        a.ste_kv_idx[pos] = k;
+        a.ste_kv_mask[pos] = m;
+        a.ste_kv_class[pos] = c;
+      }
     }
     __syncthreads();
     for (int cc = threadIdx.x; cc < kClasses; cc += blockDim.x) {
@@ -1090,7 +1120,7 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_ste_write_kernel(HierDe
   }
   int n = 0;
   for (int c = 0; c < kClasses; ++c) n += w.s_cnt[g * kClasses + c];
-  for (int p = n + threadIdx.x; p < padded; p += blockDim.x) {
+  for (int p = n + threadIdx.x; p < padded && base + p < lim; p += blockDim.x) {
     a.ste_kv_idx[base + p] = 0;
     a.ste_kv_mask[base + p] = 0;
     a.ste_kv_class[base + p] = 0;
@@ -1099,9 +1129,10 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_ste_write_kernel(HierDe
   const int first = w.grp_first[g], end = w.grp_first[g + 1];
   for (int i = first + threadIdx.x; i < end; i += blockDim.x) {
     const int64_t o = w.s_item_off[g] + (i - first);
+    if (o >= item_lim) break;
     for (int e = 0; e < 8; ++e) a.ste_items[8 * o + e] = a.items[8 * (int64_t)i + e];
     a.ste_items[8 * o + 5] = (int32_t)base;
-    a.ste_items[8 * o + 6] = padded;
+    a.ste_items[8 * o + 6] = base + padded <= lim ? padded : 0;
   }
 }
 
@@ -1109,10 +1140,14 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_ste_write_kernel(HierDe
 __global__ void derive_key_items_kernel(HierDeriveArgs a, DeriveWs w) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= a.n_items) return;
-  const int g = w.grp_of_item[i];
   for (int e = 0; e < 8; ++e) a.key_items[8 * (int64_t)i + e] = a.items[8 * (int64_t)i + e];
-  a.key_items[8 * (int64_t)i + 5] = (int32_t)w.t_off[g];
-  a.key_items[8 * (int64_t)i + 6] = w.t_size[g];
+  // a flagged pass 1 or a list past the caller's size: an empty list (the
+  // backward then reads nothing through this item)
+  const bool ok = a.totals[4] == 0;
+  const int g = ok ? w.grp_of_item[i] : 0;
+  const bool fits = ok && w.t_off[g] + w.t_size[g] <= a.key_entries;
+  a.key_items[8 * (int64_t)i + 5] = fits ? (int32_t)w.t_off[g] : 0;
+  a.key_items[8 * (int64_t)i + 6] = fits ? w.t_size[g] : 0;
 }
 
 // AND of the masks of every 64 entries (one wave per tile).
@@ -1130,7 +1165,7 @@ int derive_validate(const HierDeriveArgs* a, DeriveWs* w) {
                    a->nq_max <= 32,
                HIER_EINVAL, "invalid n_items=%d n_groups=%d rows=%d nq_max=%d", a->n_items,
                a->n_groups, a->rows, a->nq_max);
-  HIER_REQUIRE((int64_t)a->n_groups * a->n_groups * a->nq_max <= kMaxTable, HIER_EUNSUPPORTED,
+  HIER_REQUIRE((int64_t)a->n_groups * a->n_groups <= kMaxTable / a->nq_max, HIER_EUNSUPPORTED,
                "too many groups for the device transposer (%d groups x %d frames)", a->n_groups,
                a->nq_max);
   HIER_REQUIRE(a->kv_len >= 0, HIER_EINVAL, "invalid kv_len=%d", a->kv_len);
@@ -1152,7 +1187,7 @@ void fill(int32_t* p, int64_t n, int32_t v, hipStream_t s) {
 }  // namespace
 
 extern "C" int64_t hier_derive_workspace(const HierDeriveArgs* args) {
-  if (!args) return -1;
+  if (!args || !derive_sizes_ok(*args)) return -1;
   HierDeriveArgs a = *args;
   a.ws = nullptr;
   return derive_ws_layout(a, nullptr);

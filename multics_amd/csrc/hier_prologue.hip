@@ -514,8 +514,8 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   hier::clear_error();
   HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
   const HierPrologueArgs& a = *args;
-  HIER_REQUIRE(a.S >= 0 && a.H >= 1 && (a.D == 64 || a.D == 128), HIER_EUNSUPPORTED,
-               "prologue supports head_dim 64/128, got H=%d D=%d", a.H, a.D);
+  HIER_REQUIRE(a.S >= 0 && a.H >= 1 && a.H <= 4096 && (a.D == 64 || a.D == 128),
+               HIER_EUNSUPPORTED, "prologue supports head_dim 64/128, got H=%d D=%d", a.H, a.D);
   const int dim = a.H * a.D;
   const int kCPT = dim <= 3072 ? 4 : 8;
   const int nthr = dim / kCPT;
@@ -528,8 +528,12 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   HIER_REQUIRE(a.qx && a.kx && a.norm_q_w && a.norm_k_w && a.rope_cos && a.rope_sin && a.q_out &&
                    a.k_out && (!a.v_out || a.vx),
                HIER_EINVAL, "NULL tensor pointer");
-  HIER_REQUIRE(a.out_stride_s % kCPT == 0 && a.out_stride_h % kCPT == 0, HIER_EINVAL,
-               "output strides must keep %d-byte alignment", 2 * kCPT);
+  HIER_REQUIRE(a.out_stride_s % kCPT == 0 && a.out_stride_h % kCPT == 0 && a.out_stride_s >= 0 &&
+                   a.out_stride_h >= 0,
+               HIER_EINVAL, "output strides must be non-negative and keep %d-byte alignment",
+               2 * kCPT);
+  HIER_REQUIRE(hier::span_bytes(a.S, a.out_stride_s, a.out_stride_h, a.H, a.D) <= ((__int128)1 << 48),
+               HIER_EUNSUPPORTED, "output view spans more than 2^48 bytes");
   const bool cam = a.cam != nullptr;
   HIER_REQUIRE(!cam || (a.C == 12 && a.w_cam_q && a.w_cam_k), HIER_EUNSUPPORTED,
                "camera adapter supports C=12 with both weights, got C=%d", a.C);
@@ -543,7 +547,7 @@ extern "C" int hier_qkv_prologue(const HierPrologueArgs* args, void* stream) {
   const bool v = a.v_out != nullptr;
   const int nch = dim / 512;
   // the wave kernel forms output offsets in 32 bits
-  const int64_t out_ext = (int64_t)(a.S - 1) * a.out_stride_s + (int64_t)(a.H - 1) * a.out_stride_h + a.D;
+  const int64_t out_ext = (int64_t)(hier::span_bytes(a.S, a.out_stride_s, a.out_stride_h, a.H, a.D) / 2);
   if (dim % 512 == 0 && (nch <= 4 || nch == 6 || nch == 8) && a.out_stride_s % 8 == 0 &&
       a.out_stride_h % 8 == 0 && a.out_stride_s >= 0 && a.out_stride_h >= 0 && out_ext <= INT32_MAX &&
       (!cam || (((uintptr_t)a.w_cam_q | (uintptr_t)a.w_cam_k) & 15u) == 0)) {

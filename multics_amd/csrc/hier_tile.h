@@ -124,7 +124,7 @@ __device__ __forceinline__ Idx<D> load_idx(const int32_t* idx, int tile, int idx
 // multiply: the entry points check this bound on the views they copy from
 // (their 4 GiB span bound then keeps the product within 32 bits).
 __host__ __device__ constexpr bool copy_rows_ok(int64_t rows, int64_t row_stride_elems) {
-  return rows <= (1ll << 24) && row_stride_elems * 2 < (1ll << 24);
+  return rows <= (1ll << 24) && row_stride_elems < (1ll << 23);
 }
 
 // The LDS DMA instructions are issued from inline assembly.  Issued through

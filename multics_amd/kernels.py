@@ -89,18 +89,31 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
 STE_CLASSES = 16
 
 
+# Value written into output buffers that the kernels are expected to overwrite
+# entirely (see _covers_all_rows); None leaves them uninitialised.  Tests set
+# NaN to show that every row is written.
+_UNCLEARED_FILL: Optional[float] = None
+
+
+def _uncleared(like: torch.Tensor = None, *, shape=None, dtype=None, device=None) -> torch.Tensor:
+    """A buffer every row of which a kernel writes (``torch.empty``, or filled
+    with ``_UNCLEARED_FILL`` when a test sets it)."""
+    t = torch.empty_like(like) if like is not None else \
+        torch.empty(shape, dtype=dtype, device=device)
+    if _UNCLEARED_FILL is not None:
+        t.fill_(_UNCLEARED_FILL)
+    return t
+
+
 def _covers_all_rows(tiles: TileList) -> bool:
-    """Whether the items of a full-sequence list own every row once: their row
-    counts sum to the row extent (the list builders give each token to one
-    (block, stream) group and split a group's rows between its items), and
-    queries and keys are the same rows.  Then dq_kernel writes every row of
-    dQ and dkv_kernel every row of dK / dV.  Cached on the list."""
-    hit = tiles.__dict__.get("_covers_rows")
-    if hit is None:
-        rows = tiles.items[:tiles.n_items, 4].to(torch.int64).sum().item() if tiles.n_items else 0
-        hit = tiles.row_extent == tiles.key_extent and rows == tiles.row_extent
-        tiles.__dict__["_covers_rows"] = hit
-    return hit
+    """Whether the items of a full-sequence list own every row of
+    [0, row_extent) exactly once, with queries and keys the same rows.  The
+    builder records the first fact from the groups' row descriptors when it
+    builds the list (``rows_exact_cover``; derived key-major lists keep the
+    forward items' descriptors, so they inherit it).  Then dq_kernel writes
+    every row of dQ, the forward every row of O and LSE, and dkv_kernel every
+    key row of dK / dV over the key-major list."""
+    return bool(tiles.rows_exact_cover) and tiles.row_extent == tiles.key_extent
 
 
 def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
@@ -165,14 +178,15 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     if ste_geometry is not None and not list_ste:
         cls = ste_classes(tiles, ste_geometry)
     dev = q.device
-    # every row the kernels own is written; the buffers need clearing only
-    # when some row of q / k / v belongs to no work item
-    full = _covers_all_rows(tiles) and q3.shape[0] == tiles.row_extent and \
-        k3.shape[0] == tiles.key_extent and v3.shape[0] == tiles.key_extent
-    alloc = torch.empty_like if full else torch.zeros_like
-    dq = alloc(q3)
-    dk = alloc(k3)
-    dv = alloc(v3)
+    # every row the kernels own is written; a buffer needs clearing only when
+    # some of its rows belongs to no work item: dQ over the forward list,
+    # dK / dV over the key-major list (a caller's key_tiles included)
+    full_q = _covers_all_rows(tiles) and q3.shape[0] == tiles.row_extent
+    full_kv = _covers_all_rows(kt) and kt.row_extent == tiles.key_extent and \
+        k3.shape[0] == kt.row_extent and v3.shape[0] == kt.row_extent
+    dq = _uncleared(q3) if full_q else torch.zeros_like(q3)
+    dk = _uncleared(k3) if full_kv else torch.zeros_like(k3)
+    dv = _uncleared(v3) if full_kv else torch.zeros_like(v3)
     ws = None if no_alloc_workspace else \
         torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
     if ste_geometry is not None:
@@ -250,8 +264,8 @@ class HierAttentionFunction(torch.autograd.Function):
         if _covers_all_rows(tiles) and q3.shape[0] == tiles.row_extent:
             # the kernel writes every row's output and LSE (0 and -inf for a
             # row that sees no key)
-            out = torch.empty_like(q)
-            lse = torch.empty((H, q3.shape[0]), dtype=torch.float32, device=q.device)
+            out = _uncleared(q)
+            lse = _uncleared(shape=(H, q3.shape[0]), dtype=torch.float32, device=q.device)
         else:
             out = torch.zeros_like(q)
             lse = torch.full((H, q3.shape[0]), float("-inf"), dtype=torch.float32, device=q.device)

@@ -59,6 +59,9 @@ class TileList:
     row_extent: int = 0          # 1 + largest Q/O row index any item can address
     rows_per_item: int = ROWS_PER_ITEM
     frames_per_group: int = 0    # query frames of every (block, stream) group; 0 = unknown
+    # the items' rows are every row of [0, row_extent) exactly once (recorded
+    # by the builder from the groups' row descriptors; False = not known)
+    rows_exact_cover: bool = False
 
 
 @dataclass(frozen=True)
@@ -358,6 +361,32 @@ class _Upload:
         return buf
 
 
+def group_rows_cover(topo: BlockTopology):
+    """``(row_extent, exact)``: 1 + the largest query row of the tile list
+    built from ``topo``, and whether its (block, stream) groups' query rows
+    -- ``tile_qbase + j * qstride + i`` for frame j < n and row i < qlen --
+    are every row of ``[0, row_extent)`` exactly once.  The builder splits
+    each group's rows into consecutive item ranges, so its items then own
+    every row once.  Host arithmetic on the topology; no device access."""
+    P, N, n, NS = topo.P, topo.N, topo.n_frames, topo.P + topo.N + 1
+    row_ext = 0
+    group_rows = []
+    for b in range(topo.B):
+        for s_ in range(NS):
+            ql = _qlen(topo, s_)
+            if ql > 0:
+                kind = 0 if s_ < P else (1 if s_ < P + N else 2)
+                row_ext = max(row_ext, topo.tile_qbase[b][s_] + (n - 1) * topo.tile_qstride[kind] + ql)
+                group_rows.append(topo.tile_qbase[b][s_] + topo.tile_qstride[kind] *
+                                  np.arange(n, dtype=np.int64)[:, None] +
+                                  np.arange(ql, dtype=np.int64)[None, :])
+    all_rows = np.concatenate([g.ravel() for g in group_rows]) if group_rows else \
+        np.zeros(0, np.int64)
+    exact = bool(len(all_rows) == row_ext and (len(all_rows) == 0 or (
+        all_rows.min() >= 0 and np.bincount(all_rows, minlength=row_ext).max() == 1)))
+    return int(row_ext), exact
+
+
 def _item_order(P: int, N: int, B: int):
     """(stream, block) order of the work items: local hubs, global, players,
     each over all blocks."""
@@ -545,17 +574,12 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
             flat = [x for r in rows_ for x in (r if isinstance(r, (list, tuple)) else [r])]
             if flat and w > 0:
                 key_ext = max(key_ext, max(flat) + w)
-    row_ext = 0
-    for b in range(B):
-        for s_ in range(NS):
-            ql = _qlen(topo, s_)
-            if ql > 0:
-                kind = 0 if s_ < P else (1 if s_ < P + N else 2)
-                row_ext = max(row_ext, topo.tile_qbase[b][s_] + (n - 1) * topo.tile_qstride[kind] + ql)
+    row_ext, exact = group_rows_cover(topo)
     tiles = TileList(items=items[:n_items], kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
                      n_items=n_items, item_ranges=ranges, logical_pairs=int(pairs.sum()),
                      key_extent=int(key_ext), row_extent=int(row_ext),
-                     rows_per_item=rows_per_item, frames_per_group=int(n))
+                     rows_per_item=rows_per_item, frames_per_group=int(n),
+                     rows_exact_cover=exact)
     tiles._keepalive = (dv, keep)  # device inputs must outlive the async build
     layouts = None
     if tiled_res is not None:
@@ -672,7 +696,7 @@ def transpose_tiles_host(tiles: TileList) -> TileList:
                    kv_idx=to_dev(q_idx), kv_mask=to_dev(q_mask), blk_and=to_dev(blk_and),
                    n_items=tiles.n_items, item_ranges=tiles.item_ranges,
                    logical_pairs=pairs, key_extent=tiles.row_extent, row_extent=tiles.key_extent,
-                   rows_per_item=tiles.rows_per_item)
+                   rows_per_item=tiles.rows_per_item, rows_exact_cover=tiles.rows_exact_cover)
     return out
 
 
@@ -861,7 +885,7 @@ def _derive_device(tiles: TileList, ste_geometry):
     kt = TileList(items=k_items, kv_idx=k_idx, kv_mask=k_mask, blk_and=k_blk,
                   n_items=tiles.n_items, item_ranges=tiles.item_ranges, logical_pairs=pairs,
                   key_extent=tiles.row_extent, row_extent=tiles.key_extent,
-                  rows_per_item=tiles.rows_per_item)
+                  rows_per_item=tiles.rows_per_item, rows_exact_cover=tiles.rows_exact_cover)
     ste = None
     if n_ste_items > 0:
         lst = TileList(items=s_items, kv_idx=s_idx, kv_mask=s_mask, blk_and=s_blk,
@@ -1126,68 +1150,75 @@ def _get_varlen_plan(*, kv_index, kv_count, qbase, qlen, seg_ids, query_tokens):
     and errors.  The segments must partition the query rows
     ``[0, query_tokens)`` exactly (``AssertionError`` otherwise); active
     segments (rows and keys both non-empty) are flattened into ``q_index`` /
-    ``k_index`` (int64) with int32 offsets ``cu_q`` / ``cu_k``.  The flattening
-    runs as device gathers (no per-row host loop); the plan is cached by the
-    source tensors' data pointers and keeps references to them, so a reused
-    allocation cannot alias a stale plan (WAN_HIER_PACKED_PLAN_CACHE_SIZE,
-    default 64, as the reference)."""
+    ``k_index`` (int64) with int32 offsets ``cu_q`` / ``cu_k``.
+
+    Validation, flattening and the index range run where the arrays live;
+    the host reads back one vector of nine integers per cache miss (the
+    checks' outcome, the active-segment count, the flat sizes, the maxima and
+    the key index range), which the plan's Python ints and tensor shapes
+    need.  The plan is cached by the source tensors' data pointers and keeps
+    references to them, so a reused allocation cannot alias a stale plan
+    (WAN_HIER_PACKED_PLAN_CACHE_SIZE, default 64, as the reference)."""
     dev = kv_index.device
     key = (str(dev), kv_index.data_ptr(), kv_count.data_ptr(), qbase.data_ptr(), qlen.data_ptr(),
            seg_ids.data_ptr(), int(query_tokens))
     hit = _lru_get(_PLAN_CACHE, key)
     if hit is not None:
         return hit
-    qb = qbase.detach().to("cpu", torch.int64).numpy()
-    qn = qlen.detach().to("cpu", torch.int64).numpy()
-    si = seg_ids.detach().to("cpu", torch.int64).numpy()
-    nk = kv_count.detach().to("cpu", torch.int64).numpy()
-    if not np.array_equal(si, np.arange(len(si))):
+    flat64 = lambda t: t.detach().reshape(-1).to(device=dev, dtype=torch.int64)
+    qb, qn, si, nk = flat64(qbase), flat64(qlen), flat64(seg_ids), flat64(kv_count)
+    n = si.numel()
+    if qb.numel() != n or qn.numel() != n:
         raise AssertionError("packed metadata must contain exactly one program per segment")
+    width = int(kv_index.shape[1]) if kv_index.dim() == 2 else 0
+    kv2 = kv_index.detach().reshape(-1, max(width, 1)).to(torch.int64)
+    ar = torch.arange(n, device=dev, dtype=torch.int64)
+    ids_ok = (si == ar).all() & torch.tensor(nk.numel() >= n and kv2.shape[0] >= n, device=dev)
     # an exact partition in program order: every non-empty program starts
-    # where the previous one ended, the first at 0, the last ends at
-    # query_tokens (empty programs cover nothing)
-    pos, ok = 0, True
-    for b, n in zip(qb.tolist(), qn.tolist()):
-        if n <= 0:
-            continue
-        if b != pos:
-            ok = False
-            break
-        pos += n
-    if not ok or pos != int(query_tokens):
+    # where the previous ones end, and together they cover query_tokens rows
+    qc = qn.clamp(min=0)
+    start = torch.cumsum(qc, 0) - qc
+    part_ok = ((qb == start) | (qc == 0)).all() & (qc.sum() == int(query_tokens))
+    nk_s = nk[:n] if nk.numel() >= n else torch.zeros(n, device=dev, dtype=torch.int64)
+    act = (qn > 0) & (nk_s > 0)
+    qa = torch.where(act, qn, 0)
+    ka_full = torch.where(act, nk_s, 0)
+    ka = ka_full.clamp(max=width)       # a count past the row width gathers the row
+    rows = kv2[:n] if kv2.shape[0] >= n else torch.zeros(n, max(width, 1), device=dev,
+                                                         dtype=torch.int64)
+    live = torch.arange(rows.shape[1], device=dev)[None, :] < ka[:, None]
+    big = torch.iinfo(torch.int64).max
+    zero = torch.zeros((), device=dev, dtype=torch.int64)
+    stats = torch.stack([
+        ids_ok.to(torch.int64), part_ok.to(torch.int64), act.sum(), qa.sum(), ka.sum(),
+        qa.max() if n else zero, ka_full.max() if n else zero,
+        torch.where(live, rows, big).min() if n else zero,
+        torch.where(live, rows, -1).max() if n else zero - 1]).cpu().tolist()
+    if not stats[0]:
+        raise AssertionError("packed metadata must contain exactly one program per segment")
+    if not stats[1]:
         raise AssertionError("packed query segments must partition the query sequence exactly")
-    act = np.nonzero((qn > 0) & (nk[si] > 0))[0]
-    qa, ka = qn[act], nk[si[act]]
-    cu_q = np.concatenate([[0], np.cumsum(qa)]).astype(np.int32)
-    cu_k = np.concatenate([[0], np.cumsum(ka)]).astype(np.int32)
-    # rows: starts repeated per row plus the position inside the segment
-    rows_dev = torch.arange(int(cu_q[-1]), device=dev, dtype=torch.int64)
-    seg_of_row = torch.repeat_interleave(torch.arange(len(act), device=dev),
-                                         torch.from_numpy(qa).to(dev)) if len(act) else rows_dev
-    cuq_dev = torch.from_numpy(cu_q.astype(np.int64)).to(dev)
-    qb_act = torch.from_numpy(qb[act]).to(dev)
-    q_flat = (qb_act[seg_of_row] + rows_dev - cuq_dev[seg_of_row]) if len(act) else rows_dev
-    # keys: the first count entries of each active segment's row of kv_index
-    if len(act):
-        width = kv_index.shape[1]
-        kpos = torch.arange(int(cu_k[-1]), device=dev, dtype=torch.int64)
-        seg_of_key = torch.repeat_interleave(torch.arange(len(act), device=dev),
-                                             torch.from_numpy(ka).to(dev))
-        cuk_dev = torch.from_numpy(cu_k.astype(np.int64)).to(dev)
-        sid_act = torch.from_numpy(si[act]).to(dev)
-        flat = sid_act[seg_of_key] * width + (kpos - cuk_dev[seg_of_key])
-        k_flat = kv_index.reshape(-1)[flat].to(torch.int64)
-    else:
-        k_flat = torch.empty(0, device=dev, dtype=torch.int64)
+    n_act, tot_q, tot_k = stats[2], stats[3], stats[4]
+    # active segments in order (a stable sort moves them to the front)
+    act_idx = torch.argsort((~act).to(torch.int8), stable=True)[:n_act]
+    qa_a, ka_a = qa[act_idx], ka[act_idx]
+    cu_q = torch.cat([zero[None], torch.cumsum(qa_a, 0)])
+    cu_k = torch.cat([zero[None], torch.cumsum(ka_full[act_idx], 0)])
+    gk = torch.cat([zero[None], torch.cumsum(ka_a, 0)])
+    seg_ids_a = torch.arange(n_act, device=dev)
+    row_seg = torch.repeat_interleave(seg_ids_a, qa_a, output_size=tot_q)
+    q_flat = qb[act_idx][row_seg] + torch.arange(tot_q, device=dev) - cu_q[row_seg]
+    key_seg = torch.repeat_interleave(seg_ids_a, ka_a, output_size=tot_k)
+    k_flat = rows[act_idx][key_seg, torch.arange(tot_k, device=dev) - gk[key_seg]]
     res = {
         "q_index": q_flat,
         "k_index": k_flat,
-        "cu_q": torch.from_numpy(cu_q).to(dev),
-        "cu_k": torch.from_numpy(cu_k).to(dev),
-        "max_q": int(qa.max()) if len(act) else 0,
-        "max_k": int(ka.max()) if len(act) else 0,
-        "min_k_index": int(k_flat.min().item()) if k_flat.numel() else 0,
-        "max_k_index": int(k_flat.max().item()) if k_flat.numel() else -1,
+        "cu_q": cu_q.to(torch.int32),
+        "cu_k": cu_k.to(torch.int32),
+        "max_q": int(stats[5]),
+        "max_k": int(stats[6]),
+        "min_k_index": int(stats[7]) if tot_k else 0,
+        "max_k_index": int(stats[8]) if tot_k else -1,
         "metadata_sources": (kv_index, kv_count, qbase, qlen, seg_ids),
     }
     _lru_put(_PLAN_CACHE, key, res, "WAN_HIER_PACKED_PLAN_CACHE_SIZE", "64")

@@ -34,7 +34,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import metadata as M
-from .kernels import _covers_all_rows, hier_attention, hier_attention_forward, qkv_prologue
+from .kernels import (_covers_all_rows, _uncleared, hier_attention, hier_attention_forward,
+                      qkv_prologue)
 from .hier_masks import HierBlockMask
 from .kv_cache import stream_pool
 from .paged_cache import HierPagedKVCache
@@ -85,7 +86,7 @@ def _attn_out(tiles, s, H, D, device):
     items own every one of the s rows (the kernel then writes each, 0 for a
     row that sees no key), zero-filled otherwise."""
     if _covers_all_rows(tiles) and tiles.row_extent == s:
-        return torch.empty((s, H, D), dtype=torch.bfloat16, device=device)
+        return _uncleared(shape=(s, H, D), dtype=torch.bfloat16, device=device)
     return torch.zeros((s, H, D), dtype=torch.bfloat16, device=device)
 
 

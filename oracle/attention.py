@@ -34,10 +34,16 @@ Parity pins (tests/test_oracle_rope_camera.py, tests/test_oracle_grads.py):
 * ``camera_to_world`` / ``camera12`` -- rigid-transform identities (proper
   rotations, anchor -> [I | 0], invariance under a global rigid motion,
   1/pos_scale translation, composition).
-* ``rms_norm`` / ``camera_qk`` / ``rope_apply`` / ``project_qk`` -- the fused
-  HIP prologue matches them on > 99 % of elements bit for bit (the rest
-  1 ulp), and the module's autograd path (torch ops in the reference's order)
-  matches them through the module tests.
+* ``rms_norm`` / ``camera_qk`` / ``rope_apply`` / ``project_qk``
+  (tests/test_oracle_prologue.py) -- against implementations sharing no code
+  with them: ``torch.nn.functional.rms_norm`` over the whole model dim then
+  the bf16 gain product; the reference's bf16 ``nn.Linear`` camera adapter and
+  bf16 add; an explicit real rotation of adjacent channel pairs, plus pair-norm
+  preservation and the relative-position identity; their composition in the
+  reference's order (camera add -> norm -> RoPE).  Per-head RMS, eps outside
+  the square root, the gain before the bf16 cast, an unrounded camera term,
+  half-split RoPE pairs and the camera added after the norm are each planted
+  and rejected by the same checks.
 """
 
 from __future__ import annotations

@@ -206,3 +206,38 @@ def test_ste_in_dq_pass_equals_the_separate_pass(cfg):
     say(f"  gated sums: max |fold - separate| {(a - b).abs().max().item():.3e} (max {scale:.3e})")
     assert scale > 0 and (a != 0).any()
     assert ((a - b).abs() <= 1e-5 * scale + 1e-6 * b.abs()).all()
+
+
+@pytest.mark.parametrize("case", [CASES[3], CASES[4]], ids=[CASES[3][0], CASES[4][0]])
+def test_uncleared_buffers_are_fully_written(case, monkeypatch):
+    """When a list's items own every row, the forward output / LSE and dQ / dK
+    / dV are left uncleared.  Pre-filled with NaN instead (the test hook
+    ``_UNCLEARED_FILL``), the results equal the zero-filled path bit for bit,
+    on topologies with inactive local-hub rows (queries and keys with empty
+    lists) and membership orphans: every row is written by a kernel."""
+    need_gpu()
+    from multics_amd import kernels as K
+    rng = np.random.default_rng(11)
+    topo, full = _topology(case, rng)
+    H, D = case[9], case[10]
+    say("uncleared buffers", case[0], "S", topo.S)
+    g = torch.Generator().manual_seed(5)
+    q, k, v, dout = [(torch.randn(topo.S, H, D, generator=g) * 0.5).to(torch.bfloat16).cuda()
+                     for _ in range(4)]
+    tiles = M.build(full, "cuda").tiles
+    assert K._covers_all_rows(tiles)
+
+    def run():
+        qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+        out = hier_attention(qd, kd, vd, tiles)
+        out.backward(dout)
+        torch.cuda.synchronize()
+        return out.detach(), qd.grad, kd.grad, vd.grad
+
+    monkeypatch.setattr(K, "_UNCLEARED_FILL", float("nan"))
+    nan_run = run()
+    monkeypatch.setattr(K, "_covers_all_rows", lambda t: False)
+    zero_run = run()
+    for name, a, b in zip(("out", "dq", "dk", "dv"), nan_run, zero_run):
+        assert torch.isfinite(a.float()).all(), name
+        assert torch.equal(a, b), name

@@ -123,3 +123,39 @@ def test_dynamic_membership_tile_list_matches_dense_mask():
         for q in range(ft.S):
             exp = set() if dead[q] else set(np.nonzero(m[q])[0].tolist())
             assert rows[q] == exp, q
+
+
+def _packed_cases():
+    from tests.test_varlen_plan import _packed_cases as cases
+    return cases()
+
+
+@pytest.mark.parametrize("name", _packed_cases())
+def test_varlen_plan_on_device_arrays(name):
+    """``_get_varlen_plan`` (hier_packed_attention.py:32-102) on the device
+    arrays the HIP builder returns for a one-program-per-segment call, equal
+    to the oracle's plan of the reference's golden arrays; a second call hits
+    the plan cache."""
+    need_gpu()
+    from oracle.metadata import varlen_plan
+    from tests.test_varlen_plan import _arrays
+    say("varlen plan on device", name)
+    inp = G.inputs("seg", name)
+    ref = _arrays(name)
+    qt = int(np.asarray(ref["prog_nq"]).sum())
+    want = varlen_plan(ref["kv_index"], ref["kv_count"], ref["prog_qbase"], ref["prog_nq"],
+                       ref["prog_seg"], qt)
+    M.clear_metadata_cache()
+    M.clear_varlen_plan_cache()
+    qb, nq, sg, kv, kc, _ = _seg_call(inp)
+    assert kv.is_cuda
+    got = M._get_varlen_plan(kv_index=kv, kv_count=kc, qbase=qb, qlen=nq, seg_ids=sg,
+                             query_tokens=qt)
+    torch.cuda.synchronize()
+    for k in ("q_index", "k_index", "cu_q", "cu_k"):
+        assert got[k].is_cuda and got[k].dtype == (torch.int64 if k.endswith("index") else torch.int32)
+        assert np.array_equal(got[k].cpu().numpy(), want[k]), k
+    for k in ("max_q", "max_k", "min_k_index", "max_k_index"):
+        assert got[k] == want[k], k
+    assert M._get_varlen_plan(kv_index=kv, kv_count=kc, qbase=qb, qlen=nq, seg_ids=sg,
+                              query_tokens=qt) is got

@@ -79,3 +79,59 @@ def test_prologue_matches_oracle(camera, layout, shape):
         say(f"  max-abs {mx:.3e} mean-abs {mn:.3e} identical {same:.5f}")
         assert mx <= 2e-2 and mn <= 2e-4 and same > 0.99
     assert torch.equal(v.reshape(S, dim).cpu(), vx)
+
+
+def test_prologue_c2_full_size():
+    """The prologue exactly as ``bench.py`` times it: C2 (37,632 tokens x
+    3,072 channels, 24 heads), camera12 of the bench's seeded poses, the
+    bench's fp32 simplex RoPE table, head-major output.  Each output token
+    depends only on its own row, so sampled tokens are compared with
+    ``project_qk`` over an f64 RoPE table built by the oracle: the first and
+    last token of every (player, frame) camera run, every hub row of the
+    first, middle and last frames, and random tokens."""
+    need_gpu()
+    import bench
+    P, T, L, N, KL, KG, n, W, H, D, _ = bench.CONFIGS["c2"]
+    K = N * KL + KG
+    S, dim = P * T * L + T * K, H * D
+    dev = "cuda"
+    say("prologue c2 full size", S, dim)
+    g = torch.Generator(device=dev).manual_seed(bench.SEED + 7)
+    qx = (torch.randn(S, dim, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    kx = (torch.randn(S, dim, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    wq = (1 + 0.1 * torch.randn(dim, generator=g, device=dev)).to(torch.bfloat16)
+    wk = (1 + 0.1 * torch.randn(dim, generator=g, device=dev)).to(torch.bfloat16)
+    wcq = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
+    wck = (0.02 * torch.randn(dim, 12, generator=g, device=dev)).to(torch.bfloat16)
+    cam = bench.camera_tokens(P, T, L, K, dev)
+    cos, sin = bench.rope_tables(P, T, L, K, D, dev)
+    q, k, _ = qkv_prologue(qx, kx, None, norm_q_w=wq, norm_k_w=wk, rope_cos=cos, rope_sin=sin,
+                           num_heads=H, eps=1e-6, cam=cam, w_cam_q=wcq, w_cam_k=wck,
+                           out_layout="hsd")
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(3)
+    rows = set(rng.choice(S, 1500, replace=False).tolist())
+    for p in range(P):
+        for t in range(T):
+            base = p * T * L + t * L
+            rows |= {base, base + L - 1}
+    for t in (0, T // 2, T - 1):
+        rows |= {P * T * L + t * N * KL + i for i in range(N * KL)}
+        rows |= {P * T * L + T * N * KL + t * KG + i for i in range(KG)}
+    rows = torch.tensor(sorted(rows))
+    bands = OA.rerope_bands(D)
+    verts = OA.simplex_vertices(10, 32)
+    h, w = 11, 20
+    freqs = torch.cat([OA.player_freqs(bands, T, h, w, verts, p) for p in range(P)]
+                      + [OA.hub_freqs(bands, T, K)], 0)
+    assert freqs.shape[0] == S
+    cpu = lambda t: t.cpu()
+    rq, rk = OA.project_qk(cpu(qx)[rows], cpu(kx)[rows], norm_q_w=cpu(wq), norm_k_w=cpu(wk),
+                           freqs=freqs[rows], num_heads=H, eps=1e-6, cam=cpu(cam)[rows],
+                           w_cam_q=cpu(wcq), w_cam_k=cpu(wck))
+    for got, ref in ((q, rq), (k, rk)):
+        got = got[rows.to(dev)].reshape(len(rows), dim)
+        mx, mn = err_stats(got, ref)
+        same = (got.float().cpu() == ref).float().mean().item()
+        say(f"  {len(rows)} tokens: max-abs {mx:.3e} mean-abs {mn:.3e} identical {same:.5f}")
+        assert mx <= 2e-2 and mn <= 2e-3 and same > 0.99

@@ -60,7 +60,8 @@ def synth_forward_tiles(topo: FullTopology) -> M.TileList:
     as32 = lambda a: torch.from_numpy((a & 0xFFFFFFFF).astype(np.uint32).view(np.int32).copy())
     return M.TileList(items=torch.tensor(items, dtype=torch.int32), kv_idx=as32(idx),
                       kv_mask=as32(msk), blk_and=as32(blk), n_items=len(items), item_ranges=(),
-                      logical_pairs=pairs, key_extent=topo.S, row_extent=topo.S)
+                      logical_pairs=pairs, key_extent=topo.S, row_extent=topo.S,
+                      rows_exact_cover=True)
 
 
 def expand_key_major(kt: M.TileList, S: int) -> np.ndarray:
@@ -137,8 +138,10 @@ def test_transpose_rejects_partial_frames():
 
 
 def test_row_coverage_decides_whether_gradients_are_cleared():
-    """The backward leaves dQ / dK / dV uncleared only when its items own
-    every row once (``kernels._covers_all_rows``)."""
+    """The kernels leave their outputs uncleared only when the list's items
+    own every row once (``kernels._covers_all_rows``), a fact the builder
+    records from the groups' row descriptors (``metadata.group_rows_cover``)
+    and derived key-major lists inherit."""
     import dataclasses
     from multics_amd.kernels import _covers_all_rows
     rng = np.random.default_rng(3)
@@ -146,5 +149,33 @@ def test_row_coverage_decides_whether_gradients_are_cleared():
     tiles = synth_forward_tiles(FullTopology(4, 6, 3, 2, 2, 2, 3, 4, True, membership=mem,
                                              global_only=~mem.any(1)))
     assert _covers_all_rows(tiles)
-    fewer = dataclasses.replace(tiles, n_items=tiles.n_items - 1)
-    assert not _covers_all_rows(fewer)
+    assert _covers_all_rows(M.transpose_tiles_host(tiles))
+    assert not _covers_all_rows(dataclasses.replace(tiles, rows_exact_cover=False))
+    assert not _covers_all_rows(dataclasses.replace(tiles, key_extent=tiles.key_extent + 1))
+
+
+@pytest.mark.parametrize("kind", ["labels", "membership", "nodirect_w_all"])
+def test_group_rows_cover_full_sequence(kind):
+    """Full-sequence topologies: the groups' rows are every token once; a
+    group moved onto its neighbour's rows, or one dropped, is not a cover."""
+    import copy
+    rng = np.random.default_rng(4)
+    P, T, L, N, KL, KG, n = 4, 6, 5, 2, 2, 3, 3
+    if kind == "membership":
+        mem = rng.random((T, N, P)) < 0.5
+        topo = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=4,
+                                        direct=True, membership=mem, global_only=~mem.any(1))
+    else:
+        labels = np.array([[p % N for p in range(P)]] * T)
+        topo = M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n,
+                                        window=-1 if kind != "labels" else 4,
+                                        direct=kind == "labels", labels=labels)
+    S = P * T * L + T * (N * KL + KG)
+    assert M.group_rows_cover(topo) == (S, True)
+    moved = copy.deepcopy(topo)
+    moved.tile_qbase[1][0] = moved.tile_qbase[0][0]
+    assert not M.group_rows_cover(moved)[1]
+    short = copy.deepcopy(topo)
+    short.tile_qbase = [list(r) for r in short.tile_qbase]
+    short.KL = 0                        # the local-hub rows (mid-sequence) uncovered
+    assert not M.group_rows_cover(short)[1]
