@@ -358,6 +358,47 @@ def bench_layer(dev, steps=10, warmup=3):
                     "attention, the cos/sin table, the output buffer); GEMM FLOP 8*S*dim^2"}
 
 
+def bench_block_tail(dev, steps=10, warmup=3):
+    """C2 after the attention: the o-projection and the gated residual of the
+    DiT block, x = x + gate_msa * o(attn) (blocks.py:604-616, 661-668), for
+    the 4 x 9,240 player rows.  torch: the gate expanded per frame to every
+    token (as the block builds it) and the bf16 expression (two passes);
+    HIP: ``gated_residual`` reading the compact [P, T, dim] gate in one pass.
+    Both after the same hipBLASLt GEMM; outputs compared bit for bit."""
+    import torch.nn.functional as F
+    from multics_amd.kernels import gated_residual
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS["c2"]
+    dim = H * D
+    g = torch.Generator(device=dev).manual_seed(SEED + 3)
+    rnd = lambda *s: torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)
+    attn, x = rnd(P * T * L, dim), rnd(P, T * L, dim)
+    w_o, b_o = rnd(dim, dim) * 0.02, rnd(dim)
+    gate = rnd(P, T, dim)
+
+    def oproj():
+        return F.linear(attn, w_o, b_o).view(P, T * L, dim)
+
+    def torch_tail(y):
+        full = gate.unsqueeze(2).expand(-1, -1, L, -1).reshape(P, T * L, dim)
+        return x + full * y
+
+    y = oproj()
+    same = bool(torch.equal(torch_tail(y), gated_residual(x, gate, y)))
+    ms = {}
+    for name, fn in (("gemm", oproj), ("torch_gate", lambda: torch_tail(y)),
+                     ("hip_gate", lambda: gated_residual(x, gate, y)),
+                     ("gemm_torch_gate", lambda: torch_tail(oproj())),
+                     ("gemm_hip_gate", lambda: gated_residual(x, gate, oproj()))):
+        ms[name] = float(np.median(time_events(fn, steps, warmup)))
+    hbm = 3 * x.numel() * 2
+    return {"rows": P * T * L, "dim": dim, "bit_identical": same,
+            **{f"ms_{k}": round(v, 4) for k, v in ms.items()},
+            "hip_gate_gbs": round(hbm / (ms["hip_gate"] * 1e-3) / 1e9, 1),
+            "note": "o-projection (hipBLASLt) + gated residual x + gate_msa * y; the HIP pass "
+                    "reads x, y and the compact per-frame gate once and writes once "
+                    "(hip_gate_gbs over 3 x rows x dim x 2 B)"}
+
+
 def bench_rollout(dev, passes=10):
     """Config C4: cached rollout, 10 players, chunk = 6 latent frames = 2 blocks
     of 3 through the paged KV cache; time one denoising pass over a chunk in
@@ -629,6 +670,7 @@ def main():
             if cfg != args.config:
                 suite[f"fwd_{cfg}"] = bench_forward_cfg(cfg, dev)
         suite["layer_c2"] = bench_layer(dev)
+        suite["block_tail_c2"] = bench_block_tail(dev)
         suite["training_c5"] = bench_training(dev)
         suite["rollout_c4"] = bench_rollout(dev)
         suite["rollout_c4_cfg"] = bench_rollout_cfg(dev)

@@ -374,6 +374,29 @@ typedef struct HierFrameAttnArgs {
 
 int hier_frame_attn(const HierFrameAttnArgs* args, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Gated residual of the DiT block after self-attention,                    */
+/*   out = x + gate * y,                                                    */
+/* replacing GateModule.forward(x, gate_msa, self_attn_out)                 */
+/* (multics/models/blocks.py:31-35, applied at blocks.py:661, 668).  One     */
+/* gate row serves rows_per_gate consecutive rows (a frame's tokens share   */
+/* their player-frame's gate_msa, blocks.py:604-616).  bf16 throughout,     */
+/* bit-identical to torch's bf16 expression (product rounded to bf16, then  */
+/* the sum); out may equal x.  Row strides in elements.                     */
+/* ------------------------------------------------------------------------ */
+typedef struct HierGateArgs {
+  int64_t rows;                    /* rows of x / y / out                      */
+  int32_t dim;                     /* channels per row (multiple of 8)         */
+  int32_t rows_per_gate;           /* rows sharing one gate row (>= 1)         */
+  const uint16_t* x;               /* bf16 [rows][x_ss]                        */
+  const uint16_t* y;               /* bf16 [rows][y_ss]                        */
+  const uint16_t* gate;            /* bf16 [rows / rows_per_gate][gate_ss]     */
+  uint16_t* out;                   /* bf16 [rows][out_ss]                      */
+  int64_t x_ss, y_ss, gate_ss, out_ss;
+} HierGateArgs;
+
+int hier_gated_residual(const HierGateArgs* args, void* stream);
+
 /* Last error message of the calling thread ("" if none).                    */
 const char* hier_last_error(void);
 

@@ -115,6 +115,12 @@ class HierDeriveArgs(C.Structure):
                                   "ste_kv_class")]
 
 
+class HierGateArgs(C.Structure):
+    _fields_ = [("rows", i64), ("dim", i32), ("rows_per_gate", i32)] + \
+               [(n, vp) for n in ("x", "y", "gate", "out")] + \
+               [(n, i64) for n in ("x_ss", "y_ss", "gate_ss", "out_ss")]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
@@ -128,6 +134,7 @@ EXPORTS = {
     "hier_attn_bwd_noalloc": [C.POINTER(HierBwdArgs), vp],
     "hier_kv_append": [C.POINTER(HierPageArgs), vp],
     "hier_frame_attn": [C.POINTER(HierFrameAttnArgs), vp],
+    "hier_gated_residual": [C.POINTER(HierGateArgs), vp],
     "hier_last_error": [],
     "hier_version": [],
 }

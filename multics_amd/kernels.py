@@ -478,3 +478,46 @@ def qkv_prologue(qx: torch.Tensor, kx: torch.Tensor, vx: Optional[torch.Tensor],
         v_out=None if v is None else v.data_ptr(), out_stride_s=ss, out_stride_h=sh)
     _capi.call("hier_qkv_prologue", C.byref(args), _stream(dev))
     return q, k, v
+
+
+def gated_residual(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor, *,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x + gate * residual`` in one HIP pass (``hier_gated_residual``):
+    GateModule.forward of the DiT block (multics/models/blocks.py:31-35) as
+    applied after self-attention (blocks.py:661, 668).
+
+    ``x`` and ``residual`` are bf16 ``[..., S, dim]``.  ``gate`` is bf16 and
+    either the same shape (the reference's materialised gate) or compact,
+    ``[..., F, dim]`` with F dividing S: each of its rows serves S / F
+    consecutive rows -- a frame's tokens share their player-frame's gate_msa
+    (blocks.py:604-616) -- so the expanded gate is never built.  Bit-identical
+    to torch's bf16 expression.  ``out`` may be ``x`` (in place)."""
+    for name, t in (("x", x), ("gate", gate), ("residual", residual)):
+        if t.dtype != torch.bfloat16:
+            raise NotImplementedError(f"gated_residual supports bf16, got {name} {t.dtype}")
+        if not t.is_cuda:
+            raise NotImplementedError("gated_residual requires GPU tensors")
+    if residual.shape != x.shape or x.dim() < 2:
+        raise ValueError(f"x {tuple(x.shape)} and residual {tuple(residual.shape)} must match")
+    dim, S = x.shape[-1], x.shape[-2]
+    lead = x.shape[:-2]
+    if gate.shape[:-2] != lead or gate.shape[-1] != dim or gate.shape[-2] < 1 or \
+            S % gate.shape[-2] != 0:
+        raise ValueError(f"gate {tuple(gate.shape)} must be [..., F, {dim}] with F dividing {S}")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError("out must match x")
+    rows = x.numel() // dim
+    xs, ys, gs, os_ = (t.reshape(-1, dim) for t in (x, residual, gate, out))
+    for t in (xs, ys, gs, os_):
+        if t.stride(-1) != 1:
+            raise ValueError("gated_residual needs a unit channel stride")
+    if os_.data_ptr() != out.data_ptr():
+        raise ValueError("out must be contiguous")
+    args = _capi.HierGateArgs(rows=rows, dim=dim, rows_per_gate=S // gate.shape[-2],
+                              x=xs.data_ptr(), y=ys.data_ptr(), gate=gs.data_ptr(),
+                              out=os_.data_ptr(), x_ss=xs.stride(0), y_ss=ys.stride(0),
+                              gate_ss=gs.stride(0), out_ss=os_.stride(0))
+    _capi.call("hier_gated_residual", C.byref(args), _stream(x.device))
+    return out

@@ -34,8 +34,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import metadata as M
-from .kernels import (_covers_all_rows, _uncleared, hier_attention, hier_attention_forward,
-                      qkv_prologue)
+from .kernels import (_covers_all_rows, _uncleared, gated_residual, hier_attention,
+                      hier_attention_forward, qkv_prologue)
 from .hier_masks import HierBlockMask
 from .kv_cache import stream_pool
 from .paged_cache import HierPagedKVCache
@@ -56,6 +56,16 @@ class RMSNorm(nn.Module):
         xf = x.float()
         return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)).to(x.dtype) * \
             self.weight
+
+
+class GateModule(nn.Module):
+    """blocks.py:31-35: ``x + gate * residual``, on the HIP gated-residual pass
+    (``kernels.gated_residual``; bf16 GPU tensors).  ``gate`` is the
+    reference's materialised gate (same shape as ``x``) or the compact
+    per-frame gate ``[..., F, dim]``."""
+
+    def forward(self, x, gate, residual):
+        return gated_residual(x, gate, residual)
 
 
 class CompatibleLinear(nn.Linear):

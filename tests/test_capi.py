@@ -23,6 +23,7 @@ STRUCTS = {
     "HierPageArgs": _capi.HierPageArgs,
     "HierFrameAttnArgs": _capi.HierFrameAttnArgs,
     "HierDeriveArgs": _capi.HierDeriveArgs,
+    "HierGateArgs": _capi.HierGateArgs,
 }
 
 
