@@ -265,11 +265,22 @@ def bench_training(dev, steps=10, warmup=3):
         q.grad = k.grad = v.grad = lg.grad = None
         fwd().backward(dout)
 
+    from multics_amd import metadata as M
+    plan = M.MembershipLogitsPlan(device=dev, P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                  direct=True)
+
     def rebuild():
-        """The lists of the current logits, built from scratch (no cache):
-        membership read back, both device metadata passes, both device
-        key-major passes and the STE classes of the forward list."""
-        from multics_amd import metadata as M
+        """The lists of the current logits rebuilt on the device with no
+        host read-back (``MembershipLogitsPlan``): membership from the
+        logits, the tile-list pass, both key-major passes, the STE classes."""
+        t_ = plan.build(lg)
+        M.ste_classes(t_, geo)
+        return t_
+
+    def rebuild_host():
+        """The same lists through the host topology: membership read back,
+        both metadata passes (count read-back), both key-major passes (totals
+        read-back), the STE classes."""
         m = (lg.detach() > 0).cpu().numpy()
         t_ = M.build(M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
                                               direct=True, membership=m, global_only=~m.any(1)),
@@ -286,6 +297,7 @@ def bench_training(dev, steps=10, warmup=3):
     ms_fwd = float(np.median(time_events(lambda: fwd(), steps, warmup)))
     ms_step = float(np.median(time_events(step, steps, warmup)))
     ms_meta = float(np.median(time_events(rebuild, steps, warmup)))
+    ms_meta_host = float(np.median(time_events(rebuild_host, steps, warmup)))
     ms_step_rebuild = float(np.median(time_events(step_rebuild, steps, warmup)))
     E = tiles.logical_pairs
     flop_f, flop_b = 4.0 * H * D * E, 10.0 * H * D * E
@@ -294,15 +306,17 @@ def bench_training(dev, steps=10, warmup=3):
             "ms_fwd": round(ms_fwd, 4), "ms_fwd_bwd": round(ms_step, 4),
             "ms_bwd": round(ms_bwd, 4),
             "ms_metadata_rebuild": round(ms_meta, 4),
+            "ms_metadata_rebuild_host": round(ms_meta_host, 4),
             "ms_fwd_bwd_with_rebuild": round(ms_step_rebuild, 4),
             "useful_tflops_fwd_bwd": round((flop_f + flop_b) / (ms_step * 1e-3) / 1e12, 2),
             "useful_tflops_bwd": round(flop_b / (ms_bwd * 1e-3) / 1e12, 2),
             "note": "bwd = dQ (query-major, with the membership STE sums) + dK/dV (key-major); "
                     "useful FLOP 4*H*D*E fwd, 10*H*D*E bwd; *_rebuild: every step rebuilds "
                     "the forward and key-major lists and the STE classes from the logits on "
-                    "the device "
-                    "(membership read back, two count read-backs), as a step whose logits "
-                    "flipped membership must"}
+                    "the device with no host read-back (MembershipLogitsPlan), as a step "
+                    "whose logits flipped membership must; ms_metadata_rebuild_host: the same "
+                    "lists through the host topology (membership, count and totals read "
+                    "back)"}
 
 
 def bench_layer(dev, steps=10, warmup=3):

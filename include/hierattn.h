@@ -323,6 +323,24 @@ int hier_attn_bwd(const HierBwdArgs* args, void* stream);
 /* allocates nothing; calls that overlap on one GPU race on that array.      */
 int hier_attn_bwd_noalloc(const HierBwdArgs* args, void* stream);
 
+/* Membership-STE sums of hier_attn_bwd's ste_partial reduced over heads and */
+/* rows into the gradient layout of the membership logits [T][N][P]:        */
+/*   out[t][g][p] = sum_h sum_{l<L} partial[h][(p*T + t)*L + l][g]           */
+/*                + sum_h sum_{k<KL} partial[h][P*T*L + (t*N + g)*KL + k][p] */
+/* (full-sequence token order).  Deterministic (fixed summation order); no   */
+/* counterpart in the reference, whose membership has no gradient.  Every    */
+/* player and local-hub row of partial must be written (the dQ pass writes  */
+/* every row of every item).                                                */
+typedef struct HierSteReduceArgs {
+  int32_t H, P, T, L, N, KL;
+  int32_t classes;                 /* row stride of partial (>= P and N, <= 16) */
+  const float* partial;            /* [H][rows][classes]                       */
+  int64_t stride_h;                /* elements between heads of partial        */
+  float* out;                      /* [T][N][P] fp32                           */
+} HierSteReduceArgs;
+
+int hier_ste_reduce(const HierSteReduceArgs* args, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Paged KV cache append: copy the new K/V rows of a cached block into their */
 /* pool rows.  Replaces the per-stream rolling-cache writes and the per-call */

@@ -121,6 +121,11 @@ class HierGateArgs(C.Structure):
                [(n, i64) for n in ("x_ss", "y_ss", "gate_ss", "out_ss")]
 
 
+class HierSteReduceArgs(C.Structure):
+    _fields_ = [(n, i32) for n in ("H", "P", "T", "L", "N", "KL", "classes")] + \
+               [("partial", vp), ("stride_h", i64), ("out", vp)]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
@@ -132,6 +137,7 @@ EXPORTS = {
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],
     "hier_attn_bwd_noalloc": [C.POINTER(HierBwdArgs), vp],
+    "hier_ste_reduce": [C.POINTER(HierSteReduceArgs), vp],
     "hier_kv_append": [C.POINTER(HierPageArgs), vp],
     "hier_frame_attn": [C.POINTER(HierFrameAttnArgs), vp],
     "hier_gated_residual": [C.POINTER(HierGateArgs), vp],

@@ -1050,3 +1050,66 @@ extern "C" int hier_attn_bwd_noalloc(const HierBwdArgs* args, void* stream) {
   a.lse2 = ws + per;
   return bwd_run(a, stream);
 }
+
+// ---- membership-STE sums reduced to [T, N, P] ------------------------------
+//
+// out[t][g][p] = sum over heads and the L rows of player p at frame t of
+// partial[h][row][g]  +  sum over heads and the KL rows of local hub g at
+// frame t of partial[h][row][p]   (full-sequence token order).  One
+// workgroup per output; each thread sums a fixed strided subset, then a
+// fixed-order tree in LDS: deterministic.
+namespace {
+
+__global__ __launch_bounds__(256) void ste_reduce_kernel(HierSteReduceArgs a) {
+  __shared__ float part[256];
+  const int o = blockIdx.x;
+  const int p = o % a.P, g = (o / a.P) % a.N, t = o / (a.P * a.N);
+  const int64_t a0 = (int64_t)a.P * a.T * a.L;
+  const int n_pl = a.H * a.L, n_hub = a.H * a.KL;
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n_pl + n_hub; i += blockDim.x) {
+    if (i < n_pl) {
+      const int h = i / a.L, l = i - h * a.L;
+      const int64_t row = ((int64_t)p * a.T + t) * a.L + l;
+      s += a.partial[(int64_t)h * a.stride_h + row * a.classes + g];
+    } else {
+      const int j = i - n_pl, h = j / a.KL, k = j - h * a.KL;
+      const int64_t row = a0 + ((int64_t)t * a.N + g) * a.KL + k;
+      s += a.partial[(int64_t)h * a.stride_h + row * a.classes + p];
+    }
+  }
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) a.out[o] = part[0];
+}
+
+}  // namespace
+
+extern "C" int hier_ste_reduce(const HierSteReduceArgs* args, void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
+  const HierSteReduceArgs& a = *args;
+  HIER_REQUIRE(a.H >= 1 && a.P >= 1 && a.T >= 1 && a.L >= 1 && a.N >= 1 && a.KL >= 0 &&
+                   a.H <= (1 << 16) && a.P <= (1 << 16) && a.T <= (1 << 16) && a.L <= (1 << 20) &&
+                   a.N <= (1 << 16) && a.KL <= (1 << 20),
+               HIER_EINVAL, "invalid H=%d P=%d T=%d L=%d N=%d KL=%d", a.H, a.P, a.T, a.L, a.N,
+               a.KL);
+  HIER_REQUIRE(a.classes >= a.P && a.classes >= a.N && a.classes <= kSteClasses, HIER_EINVAL,
+               "classes must cover P and N and be at most %d, got %d", kSteClasses, a.classes);
+  const int64_t rows = (int64_t)a.P * a.T * a.L + (int64_t)a.T * a.N * a.KL;
+  HIER_REQUIRE(a.stride_h >= rows * a.classes, HIER_EINVAL,
+               "stride_h %lld below rows x classes %lld", (long long)a.stride_h,
+               (long long)(rows * a.classes));
+  HIER_REQUIRE((int64_t)a.H * a.L <= INT32_MAX / 2 && (int64_t)a.H * a.KL <= INT32_MAX / 2,
+               HIER_EUNSUPPORTED, "too many terms per sum");
+  HIER_REQUIRE(a.partial && a.out, HIER_EINVAL, "NULL pointer");
+  const int64_t n_out = (int64_t)a.T * a.N * a.P;
+  HIER_REQUIRE(n_out <= INT32_MAX, HIER_EUNSUPPORTED, "too many outputs");
+  hipLaunchKernelGGL(ste_reduce_kernel, dim3((unsigned)n_out), dim3(256), 0, (hipStream_t)stream,
+                     a);
+  return hier::check_launch("ste_reduce_kernel");
+}

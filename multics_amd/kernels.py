@@ -95,11 +95,11 @@ STE_CLASSES = 16
 _UNCLEARED_FILL: Optional[float] = None
 
 
-def _uncleared(like: torch.Tensor = None, *, shape=None, dtype=None, device=None) -> torch.Tensor:
+def _uncleared(like: torch.Tensor = None, *, size=None, dtype=None, device=None) -> torch.Tensor:
     """A buffer every row of which a kernel writes (``torch.empty``, or filled
     with ``_UNCLEARED_FILL`` when a test sets it)."""
     t = torch.empty_like(like) if like is not None else \
-        torch.empty(shape, dtype=dtype, device=device)
+        torch.empty(size, dtype=dtype, device=device)
     if _UNCLEARED_FILL is not None:
         t.fill_(_UNCLEARED_FILL)
     return t
@@ -187,11 +187,18 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     dq = _uncleared(q3) if full_q else torch.zeros_like(q3)
     dk = _uncleared(k3) if full_kv else torch.zeros_like(k3)
     dv = _uncleared(v3) if full_kv else torch.zeros_like(v3)
-    ws = None if no_alloc_workspace else \
-        torch.zeros((2, H, lse.shape[1]), dtype=torch.float32, device=dev)
+    # delta / lse2 of every query row are written by the dQ pass before the
+    # key-major pass reads them; rows of no item read as 0 from a cleared buffer
+    ws = None
+    if not no_alloc_workspace:
+        wshape = dict(size=(2, H, lse.shape[1]), dtype=torch.float32, device=dev)
+        ws = _uncleared(**wshape) if full_q else torch.zeros(**wshape)
     if ste_geometry is not None:
         n_cls = max(P_, N_)     # classes are groups (player rows) or players (hub rows)
-        partial = torch.zeros((H, tiles.row_extent, n_cls), dtype=torch.float32, device=dev)
+        # the dQ pass writes every row of every item; the STE-list pass only
+        # the rows of its items
+        pshape = dict(size=(H, tiles.row_extent, n_cls), dtype=torch.float32, device=dev)
+        partial = _uncleared(**pshape) if full_q and not list_ste else torch.zeros(**pshape)
     args = _capi.HierBwdArgs(
         H=H, D=D, n_items=tiles.n_items, n_key_items=kt.n_items,
         scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
@@ -224,11 +231,12 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     if ste_geometry is None:
         return res
     P_, T_, L_, N_, KL_ = (int(x) for x in ste_geometry)
-    a0 = P_ * T_ * L_
-    g_player = partial[:, :a0].reshape(H, P_, T_, L_, n_cls).sum(dim=(0, 3))[..., :N_]
-    g_local = partial[:, a0:a0 + T_ * N_ * KL_].reshape(H, T_, N_, KL_, n_cls)
-    g_local = g_local.sum(dim=(0, 3))[..., :P_]
-    return res + (g_player.permute(1, 2, 0) + g_local,)
+    sums = torch.empty((T_, N_, P_), dtype=torch.float32, device=dev)
+    red = _capi.HierSteReduceArgs(H=H, P=P_, T=T_, L=L_, N=N_, KL=KL_, classes=n_cls,
+                                  partial=partial.data_ptr(), stride_h=partial.stride(0),
+                                  out=sums.data_ptr())
+    _capi.call("hier_ste_reduce", C.byref(red), _stream(dev))
+    return res + (sums,)
 
 
 def membership_grad(logits: torch.Tensor, gated_ds: torch.Tensor) -> torch.Tensor:
@@ -265,7 +273,7 @@ class HierAttentionFunction(torch.autograd.Function):
             # the kernel writes every row's output and LSE (0 and -inf for a
             # row that sees no key)
             out = _uncleared(q)
-            lse = _uncleared(shape=(H, q3.shape[0]), dtype=torch.float32, device=q.device)
+            lse = _uncleared(size=(H, q3.shape[0]), dtype=torch.float32, device=q.device)
         else:
             out = torch.zeros_like(q)
             lse = torch.full((H, q3.shape[0]), float("-inf"), dtype=torch.float32, device=q.device)

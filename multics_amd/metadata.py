@@ -393,13 +393,10 @@ def _item_order(P: int, N: int, B: int):
     return [(s, b) for s in list(range(P, P + N)) + [P + N] + list(range(P)) for b in range(B)]
 
 
-def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
-          tiled: bool = False, rows_per_item: int = ROWS_PER_ITEM) -> BuildResult:
-    """Run the two device passes and return device tensors."""
-    topo.validate()
-    dev = torch.device(device)
-    if dev.type != "cuda":
-        raise NotImplementedError("the hierarchical metadata builder runs on the GPU (HIP)")
+def _topo_struct(topo: BlockTopology, dev: torch.device):
+    """``(HierTopo, device buffer)``: the builder's view of ``topo`` with all of
+    its host arrays uploaded in one transfer (the buffer must outlive every
+    launch that reads the struct)."""
     P, N, n, B = topo.P, topo.N, topo.n_frames, topo.B
     NS = P + N + 1
     fa = [len(x[0]) for x in topo.agent_frames]
@@ -446,6 +443,19 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
         t.membership = t.global_only = None
     t.ref_qstride = (C.c_int32 * 3)(*topo.ref_qstride)
     t.tile_qstride = (C.c_int32 * 3)(*topo.tile_qstride)
+    return t, dv
+
+
+def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
+          tiled: bool = False, rows_per_item: int = ROWS_PER_ITEM) -> BuildResult:
+    """Run the two device passes and return device tensors."""
+    topo.validate()
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise NotImplementedError("the hierarchical metadata builder runs on the GPU (HIP)")
+    P, N, n, B = topo.P, topo.N, topo.n_frames, topo.B
+    NS = P + N + 1
+    t, dv = _topo_struct(topo, dev)
     stream = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     n_seg = topo.n_seg
@@ -581,6 +591,7 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
                      rows_per_item=rows_per_item, frames_per_group=int(n),
                      rows_exact_cover=exact)
     tiles._keepalive = (dv, keep)  # device inputs must outlive the async build
+    tiles._layout = (tile_off[:-1].copy(), item_start.reshape(-1).copy())   # per (block, stream)
     layouts = None
     if tiled_res is not None:
         layouts = [HierTiledBlockLayout(tiles=tiles, block=b, **d) for b, d in enumerate(tiled_res)]
@@ -1053,6 +1064,150 @@ def full_sequence_tiles(*, device, P, T, L, N, KL, KG, n, window, direct, labels
         hit = build(topo, device).tiles
         _lru_put(_LAYOUT_CACHE, key, hit, "WAN_HIER_TILED_LAYOUT_CACHE_SIZE", "2")
     return hit
+
+
+class MembershipLogitsPlan:
+    """Per-step lists of a full-sequence membership topology whose membership
+    is ``logits > 0`` of soft logits on the device -- the training case, where
+    the reference rebuilds its mask on every forward
+    (multics/models/wan_video_dit.py:633-679) -- built without any host
+    read-back.
+
+    The geometry's superset topology (every membership bit and every
+    global-only bit on) admits every edge any membership can produce: the
+    edge rule is monotone in the membership bits except the global-only
+    edges, which the superset holds as well.  Its lists are built once; their
+    per-(block, stream) sizes bound that stream's list under any membership,
+    so each stream keeps the superset's list offset as a fixed slot, and the
+    key-major lists fit the superset's total.  A step then
+      * derives membership, global_only, the local-slot activity and the
+        query-frame activity from the logits with device ops into the
+        topology's fixed buffers,
+      * runs the tile-list half of ``hier_meta_build`` (each list written in
+        its slot, its items carrying its true padded size),
+      * runs ``hier_derive_count`` / ``hier_derive_build`` into the bounded
+        key-major arrays (offsets scanned on the device),
+    all asynchronous on the current stream.  ``logical_pairs`` of a step's
+    list is -1 (not counted: that would need a read-back)."""
+
+    def __init__(self, *, device, P, T, L, N, KL, KG, n, window, direct, no_local=False):
+        dev = torch.device(device)
+        self.geometry = (P, T, L, N, KL, KG, n, window, bool(direct), bool(no_local))
+        self.P, self.T, self.N, self.n = P, T, N, n
+        ones = dict(membership=np.ones((T, N, P), bool), global_only=np.ones((T, P), bool))
+        sup_topo = full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=window,
+                                          direct=direct, no_local=no_local, **ones)
+        sup = build(sup_topo, dev).tiles
+        self.t, self._static = _topo_struct(sup_topo, dev)
+        B = T // n
+        fl_max = int(self.t.fl_max)
+        u8 = dict(dtype=torch.uint8, device=dev)
+        self.mem = torch.zeros((T, N, P), **u8)
+        self.go = torch.zeros((T, P), **u8)
+        self.la = torch.zeros((B, max(N, 1), max(fl_max, 1)), **u8)
+        self.qa = torch.zeros((B, n, max(N, 1)), **u8)
+        # frame of local-slot column fi of block b (padding: valid = 0)
+        kf = np.zeros((B, max(fl_max, 1)), np.int64)
+        valid = np.zeros((B, max(fl_max, 1)), bool)
+        if not no_local:
+            for b in range(B):
+                fr = sup_topo.local_frames[b][0]
+                kf[b, :len(fr)], valid[b, :len(fr)] = fr, True
+        self.la_frame = torch.from_numpy(kf).to(dev)
+        self.la_valid = torch.from_numpy(valid).to(dev)
+        self.t.membership, self.t.global_only = self.mem.data_ptr(), self.go.data_ptr()
+        self.t.local_active, self.t.q_active = self.la.data_ptr(), self.qa.data_ptr()
+        tile_off, item_start = sup._layout          # the builder reads int64 / int32
+        self._kv_off = torch.from_numpy(tile_off.astype(np.int64)).to(dev)
+        self._item_off = torch.from_numpy(item_start.astype(np.int32)).to(dev)
+        self.sup = sup
+        self.n_keys = int(sup.kv_idx.numel())
+        # key-major capacity: the superset's (one read-back, here only)
+        kt_sup, _ = backward_lists(sup, None)
+        self.key_cap = int(kt_sup.kv_idx.numel())
+        self.n_groups, self.nq = _groups_and_frames(sup)
+        a = self._derive_args(sup)
+        self.ws = torch.empty(max(int(_capi.lib().hier_derive_workspace(C.byref(a))), 1),
+                              dtype=torch.uint8, device=dev)
+        self.totals = torch.zeros(8, dtype=torch.int64, device=dev)
+
+    def _derive_args(self, tiles: TileList):
+        P, T, L, N, KL = self.geometry[:5]
+        return _capi.HierDeriveArgs(
+            n_items=tiles.n_items, n_groups=self.n_groups, rows=int(tiles.row_extent),
+            nq_max=self.nq, kv_len=int(tiles.kv_idx.numel()), P=P, T=T, L=L, N=N, KL=KL,
+            items=tiles.items.data_ptr(), kv_idx=tiles.kv_idx.data_ptr(),
+            kv_mask=tiles.kv_mask.data_ptr())
+
+    def build(self, logits: torch.Tensor) -> TileList:
+        """The forward tile list of ``logits > 0`` ([T, N, P]) with its
+        key-major list cached on it (``backward_lists``)."""
+        P, T, N, n = self.P, self.T, self.N, self.n
+        dev = self.mem.device
+        if tuple(logits.shape) != (T, N, P):
+            raise ValueError(f"membership logits must be [T,N,P] = {(T, N, P)}")
+        m = logits.detach().to(dev) > 0
+        act = m.any(-1)                                           # [T, N]
+        self.mem.copy_(m)
+        self.go.copy_(~m.any(1))
+        if N > 0:
+            B = T // n
+            self.qa.copy_(act.view(B, n, N))
+            la = act[self.la_frame].permute(0, 2, 1) & self.la_valid[:, None, :]
+            self.la.copy_(la)
+        sup = self.sup
+        i32 = dict(dtype=torch.int32, device=dev)
+        items = torch.empty((sup.n_items, 8), **i32)
+        kv_idx = torch.empty(self.n_keys, **i32)
+        kv_mask = torch.empty(self.n_keys, **i32)
+        blk = torch.empty(max(self.n_keys // TILE_KEYS, 1), **i32)
+        out = _capi.HierMetaOut(rows_per_item=sup.rows_per_item)
+        out.tile_kv_off = self._kv_off.data_ptr()
+        out.tile_item_off = self._item_off.data_ptr()
+        out.tile_kv_idx, out.tile_kv_mask = kv_idx.data_ptr(), kv_mask.data_ptr()
+        out.tile_blk_and, out.tile_items = blk.data_ptr(), items.data_ptr()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _capi.call("hier_meta_build", C.byref(self.t), C.byref(out), stream)
+        tiles = TileList(items=items, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk,
+                         n_items=sup.n_items, item_ranges=sup.item_ranges, logical_pairs=-1,
+                         key_extent=sup.key_extent, row_extent=sup.row_extent,
+                         rows_per_item=sup.rows_per_item, frames_per_group=sup.frames_per_group,
+                         rows_exact_cover=sup.rows_exact_cover)
+        # key-major list, sized by the superset's
+        a = self._derive_args(tiles)
+        a.ws, a.ws_bytes, a.totals = self.ws.data_ptr(), int(self.ws.numel()), self.totals.data_ptr()
+        k_items = torch.empty((sup.n_items, 8), **i32)
+        k_idx = torch.empty(max(self.key_cap, 1), **i32)
+        k_mask = torch.empty(max(self.key_cap, 1), **i32)
+        k_blk = torch.empty(max(self.key_cap // TILE_KEYS, 1), **i32)
+        a.key_entries, a.ste_entries = self.key_cap, 0
+        a.key_items, a.key_q_idx = k_items.data_ptr(), k_idx.data_ptr()
+        a.key_q_mask, a.key_blk_and = k_mask.data_ptr(), k_blk.data_ptr()
+        _capi.call("hier_derive_count", C.byref(a), stream)
+        _capi.call("hier_derive_build", C.byref(a), stream)
+        kt = TileList(items=k_items, kv_idx=k_idx, kv_mask=k_mask, blk_and=k_blk,
+                      n_items=sup.n_items, item_ranges=sup.item_ranges, logical_pairs=-1,
+                      key_extent=sup.row_extent, row_extent=sup.key_extent,
+                      rows_per_item=sup.rows_per_item, rows_exact_cover=sup.rows_exact_cover)
+        tiles.__dict__["_derived"] = {None: (kt, None)}
+        tiles._keepalive = (self, a)
+        return tiles
+
+
+_PLAN_LRU: "OrderedDict[tuple, MembershipLogitsPlan]" = OrderedDict()
+
+
+def membership_logits_tiles(logits: torch.Tensor, *, P, T, L, N, KL, KG, n, window, direct,
+                            no_local=False) -> TileList:
+    """``MembershipLogitsPlan(...).build(logits)`` with the plan of the
+    geometry kept in a small LRU (WAN_HIER_TILED_LAYOUT_CACHE_SIZE)."""
+    key = (str(logits.device), P, T, L, N, KL, KG, n, window, bool(direct), bool(no_local))
+    plan = _lru_get(_PLAN_LRU, key)
+    if plan is None:
+        plan = MembershipLogitsPlan(device=logits.device, P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n,
+                                    window=window, direct=direct, no_local=no_local)
+        _lru_put(_PLAN_LRU, key, plan, "WAN_HIER_TILED_LAYOUT_CACHE_SIZE", "2")
+    return plan.build(logits)
 
 
 def cached_tiles(*, device, P, N, L, KL, KG, n_frames, n_block, local_attn, frames, tile_bases,

@@ -96,7 +96,7 @@ def _attn_out(tiles, s, H, D, device):
     items own every one of the s rows (the kernel then writes each, 0 for a
     row that sees no key), zero-filled otherwise."""
     if _covers_all_rows(tiles) and tiles.row_extent == s:
-        return _uncleared(shape=(s, H, D), dtype=torch.bfloat16, device=device)
+        return _uncleared(size=(s, H, D), dtype=torch.bfloat16, device=device)
     return torch.zeros((s, H, D), dtype=torch.bfloat16, device=device)
 
 
@@ -253,6 +253,15 @@ class SelfAttention(nn.Module):
         if membership_logits is not None:
             if tuple(membership_logits.shape) != (T, N, P):
                 raise ValueError(f"membership_logits must be [T,N,P] = {(T, N, P)}")
+            if global_only is None and active_group is None and membership_logits.is_cuda:
+                # the lists of logits > 0, rebuilt on the device every call
+                # with no host read-back
+                tiles = M.membership_logits_tiles(
+                    membership_logits, P=P, T=T, L=L, N=N, KL=KL, KG=KG,
+                    n=self.num_frame_per_block, window=self.local_attn_size,
+                    direct=direct_player, no_local=self.hier_no_local_hub)
+                return self._hier(x, freqs, tiles, cam_tokens, logits=membership_logits,
+                                  geometry=(P, T, L, N, KL))
             mem = (membership_logits.detach() > 0).cpu().numpy()
         elif membership is not None:
             mem = torch.as_tensor(membership).detach().to("cpu", torch.bool).numpy().reshape(T, N, P)

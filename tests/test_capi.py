@@ -24,6 +24,7 @@ STRUCTS = {
     "HierFrameAttnArgs": _capi.HierFrameAttnArgs,
     "HierDeriveArgs": _capi.HierDeriveArgs,
     "HierGateArgs": _capi.HierGateArgs,
+    "HierSteReduceArgs": _capi.HierSteReduceArgs,
 }
 
 

@@ -226,18 +226,30 @@ def test_uncleared_buffers_are_fully_written(case, monkeypatch):
                      for _ in range(4)]
     tiles = M.build(full, "cuda").tiles
     assert K._covers_all_rows(tiles)
+    ste = None
+    if case[-1] == "membership":
+        # logits whose hard value is the topology's membership: the STE sums
+        # (partial buffer) and the delta / lse2 workspace are uncleared too
+        P, T, N = case[1], case[2], case[4]
+        lg = torch.from_numpy(np.where(topo.membership, 1.0, -1.0) *
+                              (0.5 + rng.random((T, N, P)))).float().cuda()
+        ste = (lg, (P, T, case[3], N, case[5]))
 
     def run():
         qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
-        out = hier_attention(qd, kd, vd, tiles)
+        if ste is None:
+            out = hier_attention(qd, kd, vd, tiles)
+        else:
+            ld = ste[0].clone().requires_grad_(True)
+            out = hier_attention(qd, kd, vd, tiles, membership_logits=ld, ste_geometry=ste[1])
         out.backward(dout)
         torch.cuda.synchronize()
-        return out.detach(), qd.grad, kd.grad, vd.grad
+        return out.detach(), qd.grad, kd.grad, vd.grad, (ld.grad if ste else qd.grad)
 
     monkeypatch.setattr(K, "_UNCLEARED_FILL", float("nan"))
     nan_run = run()
     monkeypatch.setattr(K, "_covers_all_rows", lambda t: False)
     zero_run = run()
-    for name, a, b in zip(("out", "dq", "dk", "dv"), nan_run, zero_run):
+    for name, a, b in zip(("out", "dq", "dk", "dv", "dlogits"), nan_run, zero_run):
         assert torch.isfinite(a.float()).all(), name
         assert torch.equal(a, b), name

@@ -120,3 +120,73 @@ def test_device_builder_refuses_partial_frames():
         M._derive_device(bad, None)
     with pytest.raises(AssertionError):
         M.transpose_tiles_host(bad)
+
+
+def _group_lists(tiles, what):
+    """{(qbase, qstride, qlen, row_start, row_count, n): (kv_idx, kv_mask)} of
+    every item (lists by content; offsets may differ between builders)."""
+    it = tiles.items[:tiles.n_items].cpu().numpy()
+    idx = tiles.kv_idx.cpu().numpy()
+    msk = tiles.kv_mask.cpu().numpy()
+    out = {}
+    for qb, qs, ql, r0, rc, off, cnt, nf in it:
+        key = (qb, qs, ql, r0, rc, nf)
+        assert key not in out, (what, key)
+        out[key] = (idx[off:off + cnt].copy(), msk[off:off + cnt].copy())
+    return out
+
+
+def _same_groups(a, b, what):
+    ga, gb = _group_lists(a, what), _group_lists(b, what)
+    assert ga.keys() == gb.keys(), what
+    for k in ga:
+        assert np.array_equal(ga[k][0], gb[k][0]) and np.array_equal(ga[k][1], gb[k][1]), (what, k)
+
+
+@pytest.mark.parametrize("case", ["c5", "small"])
+def test_logits_plan_equals_host_topology(case):
+    """``MembershipLogitsPlan`` (lists of logits > 0 rebuilt on the device
+    with no read-back, in slots sized by the all-bits-on superset) against
+    the host-topology build of the same membership: every item's
+    descriptor, key list and masks, and every key-major list, equal; a
+    training step with the membership STE gives bit-identical outputs and
+    gradients.  Two builds in a row with different logits (the plan's
+    buffers reused)."""
+    need_gpu()
+    from multics_amd.kernels import hier_attention
+    dev = torch.device("cuda")
+    if case == "c5":
+        P, T, L, N, KL, KG, n, W, H, D, grp = bench.CONFIGS["c5"]
+        H = 2
+    else:
+        P, T, L, N, KL, KG, n, W, H, D = 5, 9, 24, 3, 2, 3, 3, 4, 2, 128
+    say("logits plan", case)
+    plan = M.MembershipLogitsPlan(device=dev, P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                  direct=True)
+    S = P * T * L + T * (N * KL + KG)
+    g = torch.Generator(device=dev).manual_seed(4)
+    q, k, v = ((torch.randn(S, H, D, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+               for _ in range(3))
+    dout = torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16)
+    geo = (P, T, L, N, KL)
+    for seed in (0, 1):
+        lg = torch.randn(T, N, P, generator=torch.Generator().manual_seed(seed)).to(dev)
+        mem = (lg > 0).cpu().numpy()
+        ref = M.build(M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                               direct=True, membership=mem,
+                                               global_only=~mem.any(1)), dev).tiles
+        got = plan.build(lg)
+        torch.cuda.synchronize()
+        _same_groups(got, ref, f"forward lists seed {seed}")
+        _same_groups(M.backward_lists(got)[0], M.backward_lists(ref)[0],
+                     f"key-major lists seed {seed}")
+        res = []
+        for tl in (got, ref):
+            qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+            ld = lg.clone().requires_grad_(True)
+            out = hier_attention(qd, kd, vd, tl, membership_logits=ld, ste_geometry=geo)
+            out.backward(dout)
+            res.append((out.detach(), qd.grad, kd.grad, vd.grad, ld.grad))
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out", "dq", "dk", "dv", "dlogits"), *res):
+            assert torch.equal(a, b), (seed, name)
