@@ -186,6 +186,27 @@ int hier_derive_build(const HierDeriveArgs* args, void* stream);
 int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class, int32_t* item_first,
                             void* stream);
 
+/* Membership-dependent topology arrays of a full-sequence membership        */
+/* topology from soft membership logits, in one launch: membership =        */
+/* logits > 0, global_only = in no group, and the query-frame / local-slot   */
+/* activity (a group is active where it has a member), as                   */
+/* _prepare_hier_membership_tensors derives them (multics/models/            */
+/* hier_masks.py:127-193); written into the arrays a HierTopo points at, so */
+/* the lists of new logits are rebuilt with no host round trip.            */
+typedef struct HierMembershipArgs {
+  int32_t T, N, P;                 /* frames, group slots, players             */
+  int32_t B, n;                    /* temporal blocks, frames per block (B*n = T) */
+  int32_t fl_max;                  /* local-slot columns per block             */
+  const float* logits;             /* [T][N][P] fp32 (DEVICE)                  */
+  const int32_t* la_frame;         /* [B][fl_max] frame of each column, < 0 = padding */
+  uint8_t* membership;             /* [T][N][P]                                */
+  uint8_t* global_only;            /* [T][P]                                   */
+  uint8_t* q_active;               /* [B][n][N]                                */
+  uint8_t* local_active;           /* [B][N][fl_max]                           */
+} HierMembershipArgs;
+
+int hier_membership_from_logits(const HierMembershipArgs* args, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Q/K/V layout prologue: camera-pose Q/K adapter, RMSNorm over all heads,  */
 /* gain and RoPE fused into one pass that writes the attention layout.       */

@@ -126,6 +126,12 @@ class HierSteReduceArgs(C.Structure):
                [("partial", vp), ("stride_h", i64), ("out", vp)]
 
 
+class HierMembershipArgs(C.Structure):
+    _fields_ = [(n, i32) for n in ("T", "N", "P", "B", "n", "fl_max")] + \
+               [(n, vp) for n in ("logits", "la_frame", "membership", "global_only", "q_active",
+                                  "local_active")]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
@@ -133,6 +139,7 @@ EXPORTS = {
     "hier_derive_count": [C.POINTER(HierDeriveArgs), vp],
     "hier_derive_build": [C.POINTER(HierDeriveArgs), vp],
     "hier_derive_ste_classes": [C.POINTER(HierDeriveArgs), vp, vp, vp],
+    "hier_membership_from_logits": [C.POINTER(HierMembershipArgs), vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],

@@ -659,6 +659,7 @@ constexpr int kDeriveThreads = 256;
 constexpr int kScanThreads = 1024;
 constexpr int kClasses = 64;            // STE classes (players or groups, <= 62)
 constexpr int64_t kMaxTable = 1ll << 26;  // n_groups^2 * nq_max table entries
+constexpr int kRunSplit = 8;            // workgroups per group list in the runs pass
 
 enum DeriveErr {
   kErrTwoGroups = 1,      // a token is a query row of two groups
@@ -723,6 +724,19 @@ __global__ void derive_fill_kernel(int32_t* p, int64_t n, int32_t v) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
     p[i] = v;
+}
+
+// Up to four fills in one launch (blockIdx.y selects the array).
+struct FillJobs {
+  int32_t* p[4];
+  int64_t n[4];
+  int32_t v[4];
+};
+__global__ void derive_fill4_kernel(FillJobs f) {
+  const int j = blockIdx.y;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < f.n[j];
+       i += (int64_t)gridDim.x * blockDim.x)
+    f.p[j][i] = f.v[j];
 }
 
 // Block-wide exclusive scan of one value per thread (kScanThreads threads).
@@ -815,6 +829,7 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_tokens_kernel(HierDeriv
 // run's last entry and sets its frame's bit in the key-major table for every
 // query frame of its mask.  A complete list has exactly qlen(key group) live
 // entries per (g, G, f) that occurs (checked by derive_key_sizes_kernel).
+// A group's list is split over gridDim.y workgroups (entries are independent).
 __global__ __launch_bounds__(kDeriveThreads) void derive_runs_kernel(HierDeriveArgs a, DeriveWs w) {
   const int g = blockIdx.x;
   const GroupDesc d = group_desc(a, w, g);
@@ -822,7 +837,7 @@ __global__ __launch_bounds__(kDeriveThreads) void derive_runs_kernel(HierDeriveA
   const int lane = threadIdx.x & 63;
   const int32_t* idx = a.kv_idx + d.off;
   const uint32_t* msk = a.kv_mask + d.off;
-  for (int i0 = 0; i0 < d.cnt; i0 += kDeriveThreads) {
+  for (int i0 = blockIdx.y * kDeriveThreads; i0 < d.cnt; i0 += gridDim.y * kDeriveThreads) {
     const int i = i0 + threadIdx.x;
     int64_t e = -1;                      // counted (g, G, f) of this entry
     const uint32_t m = i < d.cnt ? msk[i] : 0u;
@@ -1201,13 +1216,16 @@ extern "C" int hier_derive_count(const HierDeriveArgs* args, void* stream) {
   const HierDeriveArgs& a = *args;
   hipStream_t s = (hipStream_t)stream;
   const int64_t tab = (int64_t)a.n_groups * a.n_groups * a.nq_max;
-  fill(w.grp_first, (int64_t)a.n_groups + 1, 0, s);
-  fill(w.tok_g, a.rows, -1, s);
-  fill(reinterpret_cast<int32_t*>(w.table), tab, 0, s);
-  fill(w.runs, tab, 0, s);
+  FillJobs fj = {{w.grp_first, w.tok_g, reinterpret_cast<int32_t*>(w.table), w.runs},
+                 {(int64_t)a.n_groups + 1, a.rows, tab, tab},
+                 {0, -1, 0, 0}};
+  const int64_t fmax = std::max<int64_t>(std::max<int64_t>(a.n_groups + 1, a.rows), tab);
+  hipLaunchKernelGGL(derive_fill4_kernel, dim3((unsigned)std::min<int64_t>((fmax + 255) / 256, 1024), 4),
+                     dim3(256), 0, s, fj);
   hipLaunchKernelGGL(derive_groups_kernel, dim3(1), dim3(kScanThreads), 0, s, a, w);
   hipLaunchKernelGGL(derive_tokens_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
-  hipLaunchKernelGGL(derive_runs_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
+  hipLaunchKernelGGL(derive_runs_kernel, dim3(a.n_groups, kRunSplit), dim3(kDeriveThreads), 0, s,
+                     a, w);
   hipLaunchKernelGGL(derive_key_sizes_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
   hipLaunchKernelGGL(derive_ste_count_kernel, dim3(a.n_groups), dim3(kDeriveThreads), 0, s, a, w);
   hipLaunchKernelGGL(derive_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a, w);
@@ -1265,4 +1283,65 @@ extern "C" int hier_derive_build(const HierDeriveArgs* args, void* stream) {
                        a.ste_kv_mask, a.ste_blk_and, st);
   }
   return hier::check_launch("derive build kernels");
+}
+
+// ---- membership-dependent topology arrays from soft logits -----------------
+//
+// membership = logits > 0; global_only[t][p] = p in no group at t;
+// q_active[b][j][g] = group g has a member at frame b*n + j;
+// local_active[b][g][fi] = group g has a member at frame la_frame[b][fi]
+// (0 for a padding column, la_frame < 0).  The arrays a membership topology
+// derives from its membership (hier_masks.py:127-193), one launch.
+namespace {
+
+__device__ __forceinline__ bool any_member(const HierMembershipArgs& a, int t, int g) {
+  const float* l = a.logits + ((int64_t)t * a.N + g) * a.P;
+  bool any = false;
+  for (int p = 0; p < a.P; ++p) any |= l[p] > 0.f;
+  return any;
+}
+
+__global__ __launch_bounds__(256) void membership_kernel(HierMembershipArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n_mem = (int64_t)a.T * a.N * a.P, n_go = (int64_t)a.T * a.P;
+  const int64_t n_qa = (int64_t)a.B * a.n * a.N, n_la = (int64_t)a.B * a.N * a.fl_max;
+  if (i < n_mem) a.membership[i] = a.logits[i] > 0.f ? 1 : 0;
+  if (i < n_go) {
+    const int t = (int)(i / a.P), p = (int)(i % a.P);
+    bool in = false;
+    for (int g = 0; g < a.N; ++g) in |= a.logits[((int64_t)t * a.N + g) * a.P + p] > 0.f;
+    a.global_only[i] = in ? 0 : 1;
+  }
+  if (i < n_qa) {
+    const int g = (int)(i % a.N);
+    const int64_t bj = i / a.N;                       // b * n + j = the frame
+    a.q_active[i] = any_member(a, (int)bj, g) ? 1 : 0;
+  }
+  if (i < n_la) {
+    const int fi = (int)(i % a.fl_max);
+    const int64_t bg = i / a.fl_max;
+    const int g = (int)(bg % a.N), b = (int)(bg / a.N);
+    const int f = a.la_frame[(int64_t)b * a.fl_max + fi];
+    a.local_active[i] = (f >= 0 && f < a.T && any_member(a, f, g)) ? 1 : 0;
+  }
+}
+
+}  // namespace
+
+extern "C" int hier_membership_from_logits(const HierMembershipArgs* args, void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
+  const HierMembershipArgs& a = *args;
+  HIER_REQUIRE(a.T >= 1 && a.N >= 1 && a.P >= 1 && a.B >= 1 && a.n >= 1 && a.fl_max >= 0 &&
+                   a.T <= (1 << 20) && a.N <= 1024 && a.P <= 1024 && a.fl_max <= (1 << 20) &&
+                   (int64_t)a.B * a.n == a.T,
+               HIER_EINVAL, "invalid T=%d N=%d P=%d B=%d n=%d fl_max=%d", a.T, a.N, a.P, a.B, a.n,
+               a.fl_max);
+  HIER_REQUIRE(a.logits && a.membership && a.global_only && a.q_active &&
+                   (a.fl_max == 0 || (a.la_frame && a.local_active)),
+               HIER_EINVAL, "NULL pointer");
+  const int64_t n = std::max<int64_t>((int64_t)a.T * a.N * a.P, (int64_t)a.B * a.N * a.fl_max);
+  hipLaunchKernelGGL(membership_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return hier::check_launch("membership_kernel");
 }

@@ -1107,14 +1107,16 @@ class MembershipLogitsPlan:
         self.la = torch.zeros((B, max(N, 1), max(fl_max, 1)), **u8)
         self.qa = torch.zeros((B, n, max(N, 1)), **u8)
         # frame of local-slot column fi of block b (padding: valid = 0)
-        kf = np.zeros((B, max(fl_max, 1)), np.int64)
-        valid = np.zeros((B, max(fl_max, 1)), bool)
+        kf = np.full((B, max(fl_max, 1)), -1, np.int32)
         if not no_local:
             for b in range(B):
                 fr = sup_topo.local_frames[b][0]
-                kf[b, :len(fr)], valid[b, :len(fr)] = fr, True
+                kf[b, :len(fr)] = fr
         self.la_frame = torch.from_numpy(kf).to(dev)
-        self.la_valid = torch.from_numpy(valid).to(dev)
+        self._margs = _capi.HierMembershipArgs(
+            T=T, N=N, P=P, B=B, n=n, fl_max=fl_max, la_frame=self.la_frame.data_ptr(),
+            membership=self.mem.data_ptr(), global_only=self.go.data_ptr(),
+            q_active=self.qa.data_ptr(), local_active=self.la.data_ptr())
         self.t.membership, self.t.global_only = self.mem.data_ptr(), self.go.data_ptr()
         self.t.local_active, self.t.q_active = self.la.data_ptr(), self.qa.data_ptr()
         tile_off, item_start = sup._layout          # the builder reads int64 / int32
@@ -1132,10 +1134,11 @@ class MembershipLogitsPlan:
         self.totals = torch.zeros(8, dtype=torch.int64, device=dev)
 
     def _derive_args(self, tiles: TileList):
-        P, T, L, N, KL = self.geometry[:5]
+        # no STE geometry: the key-major list only (the dQ pass takes the
+        # STE classes of the forward list)
         return _capi.HierDeriveArgs(
             n_items=tiles.n_items, n_groups=self.n_groups, rows=int(tiles.row_extent),
-            nq_max=self.nq, kv_len=int(tiles.kv_idx.numel()), P=P, T=T, L=L, N=N, KL=KL,
+            nq_max=self.nq, kv_len=int(tiles.kv_idx.numel()), P=0, T=0, L=0, N=0, KL=0,
             items=tiles.items.data_ptr(), kv_idx=tiles.kv_idx.data_ptr(),
             kv_mask=tiles.kv_mask.data_ptr())
 
@@ -1146,15 +1149,10 @@ class MembershipLogitsPlan:
         dev = self.mem.device
         if tuple(logits.shape) != (T, N, P):
             raise ValueError(f"membership logits must be [T,N,P] = {(T, N, P)}")
-        m = logits.detach().to(dev) > 0
-        act = m.any(-1)                                           # [T, N]
-        self.mem.copy_(m)
-        self.go.copy_(~m.any(1))
-        if N > 0:
-            B = T // n
-            self.qa.copy_(act.view(B, n, N))
-            la = act[self.la_frame].permute(0, 2, 1) & self.la_valid[:, None, :]
-            self.la.copy_(la)
+        lg = logits.detach().to(device=dev, dtype=torch.float32).contiguous()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        self._margs.logits = lg.data_ptr()
+        _capi.call("hier_membership_from_logits", C.byref(self._margs), stream)
         sup = self.sup
         i32 = dict(dtype=torch.int32, device=dev)
         items = torch.empty((sup.n_items, 8), **i32)
@@ -1166,7 +1164,6 @@ class MembershipLogitsPlan:
         out.tile_item_off = self._item_off.data_ptr()
         out.tile_kv_idx, out.tile_kv_mask = kv_idx.data_ptr(), kv_mask.data_ptr()
         out.tile_blk_and, out.tile_items = blk.data_ptr(), items.data_ptr()
-        stream = torch.cuda.current_stream(dev).cuda_stream
         _capi.call("hier_meta_build", C.byref(self.t), C.byref(out), stream)
         tiles = TileList(items=items, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk,
                          n_items=sup.n_items, item_ranges=sup.item_ranges, logical_pairs=-1,
@@ -1190,7 +1187,7 @@ class MembershipLogitsPlan:
                       key_extent=sup.row_extent, row_extent=sup.key_extent,
                       rows_per_item=sup.rows_per_item, rows_exact_cover=sup.rows_exact_cover)
         tiles.__dict__["_derived"] = {None: (kt, None)}
-        tiles._keepalive = (self, a)
+        tiles._keepalive = (self, a, lg)
         return tiles
 
 

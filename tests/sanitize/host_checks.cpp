@@ -306,6 +306,46 @@ static void page_and_frame_checks() {
 // reach a GPU.
 extern "C" int hipGetDeviceCount(int* count);
 
+static void misc_checks() {
+  EXPECT(hier_gated_residual(nullptr, nullptr), HIER_EINVAL);
+  HierGateArgs ga;
+  std::memset(&ga, 0, sizeof(ga));
+  ga.rows = 1; ga.dim = 64; ga.rows_per_gate = 1;
+  ga.x = dev<uint16_t>(1); ga.y = dev<uint16_t>(2); ga.gate = dev<uint16_t>(3); ga.out = dev<uint16_t>(4);
+  ga.x_ss = ga.y_ss = ga.gate_ss = ga.out_ss = 64;
+  HierGateArgs gb = ga; gb.dim = 12;      EXPECT(hier_gated_residual(&gb, nullptr), HIER_EINVAL);
+  gb = ga; gb.rows_per_gate = 0;          EXPECT(hier_gated_residual(&gb, nullptr), HIER_EINVAL);
+  gb = ga; gb.y_ss = 8;                   EXPECT(hier_gated_residual(&gb, nullptr), HIER_EINVAL);
+  gb = ga; gb.gate = nullptr;             EXPECT(hier_gated_residual(&gb, nullptr), HIER_EINVAL);
+  gb = ga; gb.out = gb.out + 1;           EXPECT(hier_gated_residual(&gb, nullptr), HIER_EINVAL);
+  gb = ga; gb.rows = INT64_MAX / 2;       EXPECT(hier_gated_residual(&gb, nullptr), HIER_EUNSUPPORTED);
+  gb = ga; gb.rows = 0;                   EXPECT(hier_gated_residual(&gb, nullptr), HIER_OK);
+
+  EXPECT(hier_ste_reduce(nullptr, nullptr), HIER_EINVAL);
+  HierSteReduceArgs sr;
+  std::memset(&sr, 0, sizeof(sr));
+  sr.H = 24; sr.P = 4; sr.T = 21; sr.L = 220; sr.N = 2; sr.KL = 5; sr.classes = 4;
+  sr.partial = dev<float>(1); sr.out = dev<float>(2);
+  sr.stride_h = (int64_t)(4 * 21 * 220 + 21 * 2 * 5) * 4;
+  HierSteReduceArgs sb = sr; sb.classes = 3;   EXPECT(hier_ste_reduce(&sb, nullptr), HIER_EINVAL);
+  sb = sr; sb.classes = 17;                    EXPECT(hier_ste_reduce(&sb, nullptr), HIER_EINVAL);
+  sb = sr; sb.stride_h -= 1;                   EXPECT(hier_ste_reduce(&sb, nullptr), HIER_EINVAL);
+  sb = sr; sb.T = INT_MAX;                     EXPECT(hier_ste_reduce(&sb, nullptr), HIER_EINVAL);
+  sb = sr; sb.out = nullptr;                   EXPECT(hier_ste_reduce(&sb, nullptr), HIER_EINVAL);
+
+  EXPECT(hier_membership_from_logits(nullptr, nullptr), HIER_EINVAL);
+  HierMembershipArgs ma;
+  std::memset(&ma, 0, sizeof(ma));
+  ma.T = 21; ma.N = 2; ma.P = 4; ma.B = 7; ma.n = 3; ma.fl_max = 10;
+  ma.logits = dev<float>(1); ma.la_frame = dev<int32_t>(2); ma.membership = dev<uint8_t>(3);
+  ma.global_only = dev<uint8_t>(4); ma.q_active = dev<uint8_t>(5); ma.local_active = dev<uint8_t>(6);
+  HierMembershipArgs mb = ma; mb.B = 6;        EXPECT(hier_membership_from_logits(&mb, nullptr), HIER_EINVAL);
+  mb = ma; mb.P = INT_MAX;                     EXPECT(hier_membership_from_logits(&mb, nullptr), HIER_EINVAL);
+  mb = ma; mb.la_frame = nullptr;              EXPECT(hier_membership_from_logits(&mb, nullptr), HIER_EINVAL);
+  mb = ma; mb.T = INT_MAX; mb.B = INT_MAX; mb.n = 1;
+  EXPECT(hier_membership_from_logits(&mb, nullptr), HIER_EINVAL);
+}
+
 int main() {
   int n_dev = 0;
   if (hipGetDeviceCount(&n_dev) == 0 && n_dev > 0) {
@@ -322,6 +362,7 @@ int main() {
   derive_checks();
   prologue_checks();
   page_and_frame_checks();
+  misc_checks();
   std::printf("host checks done: %d failed\n", g_fail);
   return g_fail;
 }

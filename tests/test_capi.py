@@ -25,6 +25,7 @@ STRUCTS = {
     "HierDeriveArgs": _capi.HierDeriveArgs,
     "HierGateArgs": _capi.HierGateArgs,
     "HierSteReduceArgs": _capi.HierSteReduceArgs,
+    "HierMembershipArgs": _capi.HierMembershipArgs,
 }
 
 
