@@ -319,6 +319,70 @@ def bench_training(dev, steps=10, warmup=3):
                     "back)"}
 
 
+def bench_module_training(dev, steps=10, warmup=3):
+    """Config C5 through the drop-in module under autograd: one training step
+    (forward + backward) of ``SelfAttention.forward_hier_membership`` with
+    soft membership logits and the camera adapter -- the q / k / v GEMMs, the
+    HIP projection tail (camera, RMSNorm, gain, RoPE) forward and backward,
+    the lists of the current logits rebuilt on the device, the HIP attention
+    forward and backward with the membership STE, the o-projection.  Beside
+    it the same step with the reference's torch projection tail
+    (attention.py:355-365: fp32 RMSNorm, float64 RoPE) in place of the HIP
+    one.  Random bf16 weights, x ~ 0.5 N(0,1), dy ~ N(0,1)."""
+    from multics_amd.kernels import hier_attention
+    from multics_amd.module import SelfAttention
+    from multics_amd import metadata as M
+    from multics_amd import rope
+    P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS["c5"]
+    dim = H * D
+    logits, _, _ = grouping(grp, P, T, N, np.random.default_rng(SEED))
+    torch.manual_seed(SEED)
+    m = SelfAttention(dim, H).to(device=dev, dtype=torch.bfloat16).train()
+    m.num_frame_per_block, m.local_attn_size = n, W
+    m.enable_camera_pose_qk(12, dropout_p=0.0)
+    with torch.no_grad():
+        for lin in (m.q, m.k, m.v, m.o):
+            lin.weight.normal_(0.0, 0.02)
+        m.cam_q.weight.normal_(0.0, 0.02)
+        m.cam_k.weight.normal_(0.0, 0.02)
+    S = P * T * L + T * (N * KL + KG)
+    h, w = (11, 20) if L == 220 else (1, L)
+    bands = rope.precompute_freqs_cis_4d_wan_rerope(D)
+    verts = rope.build_simplex_vertices(10, rope.WAN_REROPE_SPLITS[1])
+    freqs = rope.build_self_attn_freqs_with_hub(bands, verts, T, h, w, "cpu", list(range(P)),
+                                                N * KL + KG).to(dev)
+    cam = camera_tokens(P, T, L, N * KL + KG, dev)[None]
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    x = (torch.randn(1, S, dim, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    dy = torch.randn(1, S, dim, generator=g, device=dev).to(torch.bfloat16)
+    lg = torch.from_numpy(logits).float().to(dev).requires_grad_(True)
+    kw = dict(num_players=P, num_frames=T, num_patches=L, num_groups=N, num_local_hub_tokens=KL,
+              num_global_hub_tokens=KG, direct_player=True, membership_logits=lg, cam_tokens=cam)
+
+    def step_hip():
+        m.zero_grad(set_to_none=True)
+        lg.grad = None
+        m.forward_hier_membership(x, freqs, **kw).backward(dy)
+
+    def step_torch_tail():
+        m.zero_grad(set_to_none=True)
+        lg.grad = None
+        tiles = M.membership_logits_tiles(lg, P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
+                                          direct=True)
+        q, k, v = (t.view(S, H, D) for t in m._project_self_attn_qkv(x, freqs, cam))
+        y = hier_attention(q, k, v, tiles, membership_logits=lg, ste_geometry=(P, T, L, N, KL))
+        m.o(y.reshape(1, S, dim)).backward(dy)
+
+    ms_hip = float(np.median(time_events(step_hip, steps, warmup)))
+    ms_torch = float(np.median(time_events(step_torch_tail, steps, warmup)))
+    return {"tokens": S, "dim": dim, "ms_step": round(ms_hip, 4),
+            "ms_step_torch_tail": round(ms_torch, 4),
+            "note": "module training step (fwd + bwd): GEMMs, projection tail (HIP fwd + bwd), "
+                    "lists rebuilt from the logits on the device, attention with membership "
+                    "STE, o-projection; ms_step_torch_tail: the same step with the reference's "
+                    "torch projection tail"}
+
+
 def bench_layer(dev, steps=10, warmup=3):
     """C2 through the drop-in module: ``SelfAttention.forward(x, freqs, mask,
     cam_tokens)`` (attention.py:436-442 signature) under no_grad, with the
@@ -686,6 +750,7 @@ def main():
         suite["layer_c2"] = bench_layer(dev)
         suite["block_tail_c2"] = bench_block_tail(dev)
         suite["training_c5"] = bench_training(dev)
+        suite["module_training_c5"] = bench_module_training(dev)
         suite["rollout_c4"] = bench_rollout(dev)
         suite["rollout_c4_cfg"] = bench_rollout_cfg(dev)
         suite["action_temporal_c4"] = bench_action_temporal(dev)

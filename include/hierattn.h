@@ -236,6 +236,44 @@ typedef struct HierPrologueArgs {
 
 int hier_qkv_prologue(const HierPrologueArgs* args, void* stream);
 
+/* Backward of hier_qkv_prologue's q and k outputs: the autograd of the     */
+/* camera add, RMSNorm, gain and RoPE (attention.py:355-365, 307-320,        */
+/* 231-242; rope.py:248-254), recomputed in fp32 from the forward's inputs: */
+/*   dz = rotate(d_out, -theta), dy = dz * w, dw += dz * bf16(a * r),        */
+/*   d_proj = r * dy - r^3 * a * sum(dy * a) / dim,                         */
+/* a = the projection plus the bf16 camera product, r = its inverse RMS.    */
+/* Writes d_proj (bf16 [S][H*D], the gradient of q(x) / k(x) and of the     */
+/* camera adapter's output) and per wave one fp32 row of gain-gradient      */
+/* partials ([hier_qk_prologue_bwd_waves][H*D], to be summed by the caller; */
+/* the camera-weight gradient is d_proj^T . cam, a plain GEMM).  Model dims */
+/* that are multiples of 512 up to 4096, head dim 64 or 128.                */
+typedef struct HierPrologueBwdArgs {
+  int32_t S, H, D;
+  float eps;
+  int32_t C;                       /* camera feature width (12) if cam          */
+  int32_t tokens_per_wave;         /* consecutive tokens per wave (>= 1)        */
+  const uint16_t* qx;              /* [S][H*D] bf16 forward inputs              */
+  const uint16_t* kx;
+  const uint16_t* cam;             /* [S][C] bf16 camera tokens or NULL         */
+  const uint16_t* w_cam_q;         /* [H*D][C] bf16                             */
+  const uint16_t* w_cam_k;
+  const uint16_t* norm_q_w;        /* [H*D] bf16 RMSNorm gains                  */
+  const uint16_t* norm_k_w;
+  const float* rope_cos;           /* [S][D/2] fp32                             */
+  const float* rope_sin;
+  const uint16_t* dq;              /* bf16 gradient of q, (s,h,d) at s*dq_ss + h*dq_sh + d */
+  const uint16_t* dk;
+  int64_t dq_ss, dq_sh, dk_ss, dk_sh;
+  uint16_t* dqx;                   /* [S][H*D] bf16 gradient of q(x)            */
+  uint16_t* dkx;
+  float* dw_q_partial;             /* [waves][H*D] fp32                         */
+  float* dw_k_partial;
+} HierPrologueBwdArgs;
+
+/* Rows of each dw_*_partial buffer for args (S, tokens_per_wave); -1 if invalid. */
+int hier_qk_prologue_bwd_waves(const HierPrologueBwdArgs* args);
+int hier_qk_prologue_bwd(const HierPrologueBwdArgs* args, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Block-sparse frame-causal flash attention forward over the tile list.    */
 /* Replaces _segmented_attn_fwd / _tiled128_fwd launches                     */

@@ -132,6 +132,15 @@ class HierMembershipArgs(C.Structure):
                                   "local_active")]
 
 
+class HierPrologueBwdArgs(C.Structure):
+    _fields_ = [("S", i32), ("H", i32), ("D", i32), ("eps", f32), ("C", i32),
+                ("tokens_per_wave", i32)] + \
+               [(n, vp) for n in ("qx", "kx", "cam", "w_cam_q", "w_cam_k", "norm_q_w", "norm_k_w",
+                                  "rope_cos", "rope_sin", "dq", "dk")] + \
+               [(n, i64) for n in ("dq_ss", "dq_sh", "dk_ss", "dk_sh")] + \
+               [(n, vp) for n in ("dqx", "dkx", "dw_q_partial", "dw_k_partial")]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
@@ -141,6 +150,8 @@ EXPORTS = {
     "hier_derive_ste_classes": [C.POINTER(HierDeriveArgs), vp, vp, vp],
     "hier_membership_from_logits": [C.POINTER(HierMembershipArgs), vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
+    "hier_qk_prologue_bwd_waves": [C.POINTER(HierPrologueBwdArgs)],
+    "hier_qk_prologue_bwd": [C.POINTER(HierPrologueBwdArgs), vp],
     "hier_attn_fwd": [C.POINTER(HierFwdArgs), vp],
     "hier_attn_bwd": [C.POINTER(HierBwdArgs), vp],
     "hier_attn_bwd_noalloc": [C.POINTER(HierBwdArgs), vp],

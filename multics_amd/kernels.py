@@ -529,3 +529,89 @@ def gated_residual(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor, 
                               gate_ss=gs.stride(0), out_ss=os_.stride(0))
     _capi.call("hier_gated_residual", C.byref(args), _stream(x.device))
     return out
+
+
+PROLOGUE_BWD_TOKENS_PER_WAVE = 16
+
+
+class QKPrologueFunction(torch.autograd.Function):
+    """Differentiable q / k projection tail on the HIP kernels: forward
+    ``hier_qkv_prologue`` (camera adapter, RMSNorm, gain, RoPE fused), backward
+    ``hier_qk_prologue_bwd`` (the same chain's gradient recomputed in fp32 from
+    the forward's inputs), plus the camera-weight gradient as the GEMM
+    ``d_proj^T . cam`` and the gains' column sums.  Replaces the autograd of
+    attention.py:355-365 / 307-320 / 231-242 and rope.py:248-254 on the
+    training path.  Inputs: ``qx, kx`` [S, H*D] bf16 (the q / k projections),
+    the RMSNorm gains, fp32 cos / sin [S, D/2], optional camera rows [S, 12]
+    and adapter weights [H*D, 12].  Returns q, k as [S, H, D] views of
+    head-major storage."""
+
+    @staticmethod
+    def forward(ctx, qx, kx, norm_q_w, norm_k_w, cam, w_cam_q, w_cam_k, rope_cos, rope_sin,
+                num_heads: int, eps: float):
+        q, k, _ = qkv_prologue(qx, kx, None, norm_q_w=norm_q_w, norm_k_w=norm_k_w,
+                               rope_cos=rope_cos, rope_sin=rope_sin, num_heads=num_heads, eps=eps,
+                               cam=cam, w_cam_q=w_cam_q, w_cam_k=w_cam_k, out_layout="hsd")
+        ctx.save_for_backward(qx, kx, norm_q_w, norm_k_w, cam, w_cam_q, w_cam_k, rope_cos,
+                              rope_sin)
+        ctx.num_heads, ctx.eps = num_heads, eps
+        return q, k
+
+    @staticmethod
+    def backward(ctx, dq, dk):
+        qx, kx, wq, wk, cam, wcq, wck, cs, sn = ctx.saved_tensors
+        H = ctx.num_heads
+        S, dim = qx.shape
+        D = dim // H
+        dev = qx.device
+        dq = torch.zeros_like(qx).view(S, H, D) if dq is None else dq
+        dk = torch.zeros_like(kx).view(S, H, D) if dk is None else dk
+        grads = []
+        for g_ in (dq, dk):
+            g_ = g_.to(torch.bfloat16)
+            if g_.stride(2) != 1 or g_.stride(0) % 8 or g_.stride(1) % 8:
+                g_ = g_.contiguous()
+            grads.append(g_)
+        dq, dk = grads
+        dqx = torch.empty_like(qx)
+        dkx = torch.empty_like(kx)
+        args = _capi.HierPrologueBwdArgs(
+            S=S, H=H, D=D, eps=float(ctx.eps), C=0 if cam is None else cam.shape[-1],
+            tokens_per_wave=PROLOGUE_BWD_TOKENS_PER_WAVE, qx=qx.data_ptr(), kx=kx.data_ptr(),
+            cam=None if cam is None else cam.data_ptr(),
+            w_cam_q=None if cam is None else wcq.data_ptr(),
+            w_cam_k=None if cam is None else wck.data_ptr(),
+            norm_q_w=wq.data_ptr(), norm_k_w=wk.data_ptr(), rope_cos=cs.data_ptr(),
+            rope_sin=sn.data_ptr(), dq=dq.data_ptr(), dk=dk.data_ptr(), dq_ss=dq.stride(0),
+            dq_sh=dq.stride(1), dk_ss=dk.stride(0), dk_sh=dk.stride(1), dqx=dqx.data_ptr(),
+            dkx=dkx.data_ptr())
+        waves = int(_capi.lib().hier_qk_prologue_bwd_waves(C.byref(args)))
+        if waves < 0:
+            raise NotImplementedError("prologue backward: too many tokens")
+        part = torch.empty((2, max(waves, 1), dim), dtype=torch.float32, device=dev)
+        args.dw_q_partial, args.dw_k_partial = part[0].data_ptr(), part[1].data_ptr()
+        _capi.call("hier_qk_prologue_bwd", C.byref(args), _stream(dev))
+        dw = part[:, :waves].sum(dim=1) if waves else torch.zeros((2, dim), device=dev)
+        dwq, dwk = (x.to(wq.dtype) for x in dw)
+        dwcq = dwck = dcam = None
+        if cam is not None:
+            if ctx.needs_input_grad[5]:
+                dwcq = torch.mm(dqx.t(), cam.to(dqx.dtype)).to(wcq.dtype)
+            if ctx.needs_input_grad[6]:
+                dwck = torch.mm(dkx.t(), cam.to(dkx.dtype)).to(wck.dtype)
+            if ctx.needs_input_grad[4]:
+                dcam = (torch.mm(dqx, wcq.to(dqx.dtype)) + torch.mm(dkx, wck.to(dkx.dtype))).to(
+                    cam.dtype)
+        return dqx, dkx, dwq, dwk, dcam, dwcq, dwck, None, None, None, None
+
+
+def qk_prologue_train(qx, kx, *, norm_q_w, norm_k_w, rope_cos, rope_sin, num_heads, eps,
+                      cam=None, w_cam_q=None, w_cam_k=None):
+    """``QKPrologueFunction.apply`` with the argument checks of
+    ``qkv_prologue``: q, k as [S, H, D] (head-major storage), differentiable
+    in the projections, the gains and the camera adapter."""
+    cs = rope_cos.contiguous().float()
+    sn = rope_sin.contiguous().float()
+    camc = None if cam is None else cam.to(torch.bfloat16).contiguous()
+    return QKPrologueFunction.apply(qx.contiguous(), kx.contiguous(), norm_q_w, norm_k_w, camc,
+                                    w_cam_q, w_cam_k, cs, sn, int(num_heads), float(eps))

@@ -35,7 +35,7 @@ import torch.nn.functional as F
 
 from . import metadata as M
 from .kernels import (_covers_all_rows, _uncleared, gated_residual, hier_attention,
-                      hier_attention_forward, qkv_prologue)
+                      hier_attention_forward, qk_prologue_train, qkv_prologue)
 from .hier_masks import HierBlockMask
 from .kv_cache import stream_pool
 from .paged_cache import HierPagedKVCache
@@ -194,6 +194,29 @@ class SelfAttention(nn.Module):
             w_cam_k=None if cam is None else self.cam_k.weight, out_layout="hsd")
         return q, k, vx.view(vx.shape[0], self.num_heads, self.head_dim)
 
+    def _project_train(self, x, freqs, cam_tokens):
+        """Differentiable [S, H, D] bf16 Q/K/V.  On the GPU, for bf16 weights and
+        model dims that are multiples of 512 (up to 4096), the q / k tail runs
+        on the HIP prologue forward and backward (``qk_prologue_train``) after
+        the three GEMMs; otherwise the reference's torch ops
+        (``_project_self_attn_qkv``)."""
+        s = x.shape[1]
+        H, D = self.num_heads, self.head_dim
+        dim = H * D
+        if self._fused_ok(x, cam_tokens) and dim % 512 == 0 and dim <= 4096:
+            cam = self._check_cam(x, cam_tokens)
+            qx, kx, vx = (lin(x)[0] for lin in (self.q, self.k, self.v))
+            cs, sn = freqs_to_cos_sin(freqs, device=x.device)
+            q, k = qk_prologue_train(
+                qx, kx, norm_q_w=self.norm_q.weight, norm_k_w=self.norm_k.weight, rope_cos=cs,
+                rope_sin=sn, num_heads=H, eps=self.norm_q.eps,
+                cam=None if cam is None else cam[0],
+                w_cam_q=None if cam is None else self.cam_q.weight,
+                w_cam_k=None if cam is None else self.cam_k.weight)
+            return q, k, vx.view(s, H, D)
+        return tuple(t.to(torch.bfloat16).view(s, H, D)
+                     for t in self._project_self_attn_qkv(x, freqs, cam_tokens))
+
     def _qkv_blocks(self, x, freqs, cam_tokens):
         """[S, H, D] bf16 Q/K/V of a [1, S, dim] input (fused prologue when it applies)."""
         s = x.shape[1]
@@ -209,10 +232,8 @@ class SelfAttention(nn.Module):
             raise NotImplementedError("hierarchical attention supports B=1")
         H, D = self.num_heads, self.head_dim
         if torch.is_grad_enabled():
-            q, k, v = self._project_self_attn_qkv(x, freqs, cam_tokens)
-            as4 = lambda t: t.to(torch.bfloat16).view(s, H, D)
-            y = hier_attention(as4(q), as4(k), as4(v), tiles, membership_logits=logits,
-                               ste_geometry=geometry)
+            q, k, v = self._project_train(x, freqs, cam_tokens)
+            y = hier_attention(q, k, v, tiles, membership_logits=logits, ste_geometry=geometry)
         else:
             q, k, v = self._qkv_blocks(x, freqs, cam_tokens)
             y = _attn_out(tiles, s, H, D, x.device)
@@ -310,8 +331,7 @@ class SelfAttention(nn.Module):
             raise ValueError(f"x has {s} tokens, the block mask covers S={mask.S}")
         H, D = self.num_heads, self.head_dim
         if torch.is_grad_enabled():
-            q, k, v = (t.to(torch.bfloat16).view(s, H, D)
-                       for t in self._project_self_attn_qkv(x, freqs, cam_tokens))
+            q, k, v = self._project_train(x, freqs, cam_tokens)
             y = hier_attention(q, k, v, mask.tiles)
         else:
             q, k, v = self._qkv_blocks(x, freqs, cam_tokens)

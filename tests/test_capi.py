@@ -26,6 +26,7 @@ STRUCTS = {
     "HierGateArgs": _capi.HierGateArgs,
     "HierSteReduceArgs": _capi.HierSteReduceArgs,
     "HierMembershipArgs": _capi.HierMembershipArgs,
+    "HierPrologueBwdArgs": _capi.HierPrologueBwdArgs,
 }
 
 

@@ -254,3 +254,66 @@ def test_flex_block_mask_path(case):
                                                   membership=torch.from_numpy(mem),
                                                   global_only=torch.from_numpy(go))))
     assert again[0] is mask
+
+
+def test_module_training_step_hip_prologue():
+    """A training step of the module at a model dim the HIP prologue backward
+    takes (512: 4 heads x 128), with the camera adapter and soft membership
+    logits: ``forward_hier_membership`` runs the GEMMs, the HIP q / k tail
+    forward and backward, the HIP attention forward and backward with the
+    membership STE and the o-projection.  Every gradient -- x, the four
+    projections (weights and biases), the RMSNorm gains, the camera adapters
+    and the logits -- against fp32 autograd of the reference module math (the
+    torch projection tail of attention.py:355-365) with the oracle attention
+    and STE.  Every gradient within 2 % of its largest entry (max error) and
+    1 % of its mean magnitude (mean error); dx and dlogits, per-token and
+    per-bit quantities, also within the north-star max-abs 2e-2 / mean-abs
+    2e-3 (per unit of the largest entry above 1).  The parameter gradients
+    are sums over all tokens of bf16 products, whose rounding noise grows
+    with the token count, so they are held to the relative bounds only."""
+    need_gpu()
+    from oracle.ste import ste_attention
+    from tests.test_gpu_prologue import _grad_check
+    P, T, L, N, KL, KG, n, W, H, D = 4, 6, 16, 2, 5, 6, 3, 4, 4, 128
+    dim = H * D
+    m = _module(dim, H, seed=21, cam=True)
+    m.num_frame_per_block, m.local_attn_size = n, W
+    rng = np.random.default_rng(22)
+    logits = torch.from_numpy(rng.standard_normal((T, N, P))).float()
+    mem = (logits > 0).numpy()
+    topo = FullTopology(P, T, L, N, KL, KG, n, W, True, membership=mem, global_only=~mem.any(1))
+    S = topo.S
+    g = torch.Generator().manual_seed(23)
+    x = (torch.randn(1, S, dim, generator=g) * 0.5).to(torch.bfloat16)
+    dy = torch.randn(1, S, dim, generator=g).to(torch.bfloat16)
+    cam = torch.zeros(1, S, 12)
+    cam[0, :P * T * L] = torch.randn(P * T * L, 12, generator=g)
+    cam = cam.to(torch.bfloat16)
+    freqs = _freqs(S, D, 24)
+    say("module training step, HIP prologue", S, dim)
+    xg = x.cuda().requires_grad_(True)
+    lg = logits.cuda().requires_grad_(True)
+    y = m.forward_hier_membership(xg, freqs, num_players=P, num_frames=T, num_patches=L,
+                                  num_groups=N, num_local_hub_tokens=KL, num_global_hub_tokens=KG,
+                                  direct_player=True, membership_logits=lg, cam_tokens=cam.cuda())
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+
+    mf = SelfAttention(dim, H, eps=1e-6)
+    mf.enable_camera_pose_qk(12, dropout_p=0.0)
+    mf.load_state_dict({k_: v_.float().cpu() for k_, v_ in m.state_dict().items()})
+    mf.num_frame_per_block, mf.local_attn_size = n, W
+    xf = x.float().requires_grad_(True)
+    lf = logits.clone().requires_grad_(True)
+    q, k, v = mf._project_self_attn_qkv(xf, freqs, cam.float())
+    att = ste_attention(q.view(S, H, D), k.view(S, H, D), v.view(S, H, D), topo, lf)
+    yf = mf.o(att.reshape(1, S, dim))
+    yf.backward(dy.float())
+    mx, mn = err_stats(y.detach(), yf.detach())
+    say(f"  output max-abs {mx:.3e} mean-abs {mn:.3e}")
+    assert mx <= 2e-2 and mn <= 2e-3
+    _grad_check("dx", xg.grad, xf.grad)
+    _grad_check("dlogits", lg.grad, lf.grad)
+    params = dict(m.named_parameters())
+    for name, p_ in mf.named_parameters():
+        _grad_check(f"d{name}", params[name].grad, p_.grad, absolute=False)

@@ -135,3 +135,81 @@ def test_prologue_c2_full_size():
         same = (got.float().cpu() == ref).float().mean().item()
         say(f"  {len(rows)} tokens: max-abs {mx:.3e} mean-abs {mn:.3e} identical {same:.5f}")
         assert mx <= 2e-2 and mn <= 2e-3 and same > 0.99
+
+
+def _grad_check(name, got, ref, rel_max=2e-2, rel_mean=1e-2, absolute=True):
+    """Relative bounds (max error within 2 % of max|ref|, mean error within
+    1 % of mean|ref|) and, with ``absolute``, the north-star absolute bounds
+    scaled to the gradient's size (max-abs <= 2e-2 and mean-abs <= 2e-3 per
+    unit of max|ref| above 1)."""
+    got = got.detach().float().cpu()
+    ref = ref.detach().float()
+    err = (got - ref).abs()
+    scale = max(1.0, ref.abs().max().item())
+    say(f"  {name}: max-abs {err.max().item():.3e} mean-abs {err.mean().item():.3e} "
+        f"(ref max {ref.abs().max().item():.3e} mean {ref.abs().mean().item():.3e})")
+    assert torch.isfinite(got).all(), name
+    if absolute:
+        assert err.max().item() <= 2e-2 * scale and err.mean().item() <= 2e-3 * scale, name
+    assert err.max().item() <= rel_max * ref.abs().max().item() + 1e-6, name
+    assert err.mean().item() <= rel_mean * ref.abs().mean().item() + 1e-7, name
+
+
+@pytest.mark.parametrize("camera", [False, True])
+@pytest.mark.parametrize("shape", ["dim512", "dim3072", "d64"])
+def test_prologue_backward_matches_fp32_autograd(camera, shape):
+    """``QKPrologueFunction`` (HIP forward and backward of the camera add,
+    RMSNorm, gain and RoPE) against torch autograd through ``project_qk`` in
+    fp32 / f64 on the CPU (the roundings of the forward pass the gradient
+    through unchanged in both): gradients of the q / k projections, the
+    RMSNorm gains and the camera-adapter weights."""
+    need_gpu()
+    from multics_amd.kernels import qk_prologue_train
+    say("prologue backward", shape, "camera", camera)
+    P, T, h, w, H, D = 2, 3, 4, 5, 4, 128
+    if shape == "dim3072":
+        T, H = 2, 24
+    elif shape == "d64":
+        H, D = 8, 64
+    K_total = 2 * 5 + 6
+    S = P * T * h * w + T * K_total
+    dim = H * D
+    g = torch.Generator().manual_seed(8)
+    qx = (torch.randn(S, dim, generator=g) * 0.5).to(torch.bfloat16)
+    kx = (torch.randn(S, dim, generator=g) * 0.5).to(torch.bfloat16)
+    wq = (1 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16)
+    wk = (1 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16)
+    freqs = _freqs(P, T, h, w, K_total)
+    if D == 64:
+        freqs = freqs[..., :32].contiguous()
+    cam = wcq = wck = None
+    if camera:
+        cam = torch.zeros(S, 12)
+        cam[:P * T * h * w] = torch.randn(P * T * h * w, 12, generator=g)
+        cam = cam.to(torch.bfloat16)
+        wcq = (0.05 * torch.randn(dim, 12, generator=g)).to(torch.bfloat16)
+        wck = (0.05 * torch.randn(dim, 12, generator=g)).to(torch.bfloat16)
+    dq = (torch.randn(S, H, D, generator=g) * 0.5).to(torch.bfloat16)
+    dk = (torch.randn(S, H, D, generator=g) * 0.5).to(torch.bfloat16)
+
+    dev = "cuda"
+    leaf = lambda t: None if t is None else t.to(dev).requires_grad_(True)
+    hq, hk, hwq, hwk, hwcq, hwck = (leaf(t) for t in (qx, kx, wq, wk, wcq, wck))
+    q, k = qk_prologue_train(hq, hk, norm_q_w=hwq, norm_k_w=hwk,
+                             rope_cos=freqs[:, 0].real.float().to(dev),
+                             rope_sin=freqs[:, 0].imag.float().to(dev), num_heads=H, eps=1e-6,
+                             cam=None if cam is None else cam.to(dev), w_cam_q=hwcq, w_cam_k=hwck)
+    torch.autograd.backward([q, k], [dq.to(dev), dk.to(dev)])
+    torch.cuda.synchronize()
+
+    f32 = lambda t: None if t is None else t.float().requires_grad_(True)
+    rq, rk, rwq, rwk, rwcq, rwck = (f32(t) for t in (qx, kx, wq, wk, wcq, wck))
+    oq, ok = OA.project_qk(rq, rk, norm_q_w=rwq, norm_k_w=rwk, freqs=freqs, num_heads=H, eps=1e-6,
+                           cam=None if cam is None else cam.float(), w_cam_q=rwcq, w_cam_k=rwck)
+    torch.autograd.backward([oq, ok], [dq.float().reshape(S, dim), dk.float().reshape(S, dim)])
+    for name, a, b in (("dqx", hq.grad, rq.grad), ("dkx", hk.grad, rk.grad),
+                       ("dnorm_q", hwq.grad, rwq.grad), ("dnorm_k", hwk.grad, rwk.grad)):
+        _grad_check(name, a, b)
+    if camera:
+        _grad_check("dcam_q", hwcq.grad, rwcq.grad)
+        _grad_check("dcam_k", hwck.grad, rwck.grad)
