@@ -186,6 +186,38 @@ int hier_derive_build(const HierDeriveArgs* args, void* stream);
 int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class, int32_t* item_first,
                             void* stream);
 
+/* Hub streams of a full-sequence tile list merged across temporal blocks:  */
+/* the rows of G consecutive blocks of one local-hub slot (or of the global */
+/* hub) become one group whose key list is the union of the G source lists, */
+/* a key's mask bits of block b0 + j shifted by n * j.  Sources are given by */
+/* one of their items (its list offset and padded size are read on the      */
+/* device); each merged list goes, in key-row order, into its slot          */
+/* [out_off, out_off + out_cap) of the same kv arrays, padded to 64 with    */
+/* mask 0, with its per-64 mask ANDs; the group's items (rows split into    */
+/* rows_per_item pieces) go to out_items at group_item_off.  acc is a       */
+/* [n_groups][rows] uint32 workspace.  No reference counterpart (the        */
+/* reference runs one program per segment: hier_tiled_attention.py:52-146). */
+typedef struct HierMergeArgs {
+  int32_t n_groups, n_src;
+  int32_t rows;                    /* key rows (1 + largest key index)         */
+  int32_t rows_per_item;
+  const int32_t* items;            /* the built list's items                   */
+  int32_t* kv_idx;                 /* the built list's arrays (sources read,   */
+  uint32_t* kv_mask;               /* merged slots written)                    */
+  uint32_t* blk_and;
+  uint32_t* acc;                   /* [n_groups][rows] workspace               */
+  const int32_t* src_item;         /* [n_src] an item of each source list      */
+  const int32_t* src_group;        /* [n_src] merged group of each source      */
+  const int32_t* src_shift;        /* [n_src] bit shift of its masks           */
+  const int64_t* out_off;          /* [n_groups] slot offsets (multiples of 64) */
+  const int32_t* out_cap;          /* [n_groups] slot capacities (multiples of 64) */
+  const int32_t* group_desc;       /* [n_groups][4] qbase, qstride, qlen, frames */
+  const int32_t* group_item_off;   /* [n_groups] first output item             */
+  int32_t* out_items;              /* [sum items][8]                           */
+} HierMergeArgs;
+
+int hier_merge_hub_lists(const HierMergeArgs* args, void* stream);
+
 /* Membership-dependent topology arrays of a full-sequence membership        */
 /* topology from soft membership logits, in one launch: membership =        */
 /* logits > 0, global_only = in no group, and the query-frame / local-slot   */

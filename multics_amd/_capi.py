@@ -141,6 +141,13 @@ class HierPrologueBwdArgs(C.Structure):
                [(n, vp) for n in ("dqx", "dkx", "dw_q_partial", "dw_k_partial")]
 
 
+class HierMergeArgs(C.Structure):
+    _fields_ = [(n, i32) for n in ("n_groups", "n_src", "rows", "rows_per_item")] + \
+               [(n, vp) for n in ("items", "kv_idx", "kv_mask", "blk_and", "acc", "src_item",
+                                  "src_group", "src_shift", "out_off", "out_cap", "group_desc",
+                                  "group_item_off", "out_items")]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
@@ -149,6 +156,7 @@ EXPORTS = {
     "hier_derive_build": [C.POINTER(HierDeriveArgs), vp],
     "hier_derive_ste_classes": [C.POINTER(HierDeriveArgs), vp, vp, vp],
     "hier_membership_from_logits": [C.POINTER(HierMembershipArgs), vp],
+    "hier_merge_hub_lists": [C.POINTER(HierMergeArgs), vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_qk_prologue_bwd_waves": [C.POINTER(HierPrologueBwdArgs)],
     "hier_qk_prologue_bwd": [C.POINTER(HierPrologueBwdArgs), vp],

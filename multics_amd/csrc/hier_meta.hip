@@ -1345,3 +1345,124 @@ extern "C" int hier_membership_from_logits(const HierMembershipArgs* args, void*
                      (hipStream_t)stream, a);
   return hier::check_launch("membership_kernel");
 }
+
+// ---- hub streams merged across temporal blocks -----------------------------
+//
+// A local-hub slot or the global hub has few query rows per block (n * KL,
+// n * KG) but a long key list, so one work item per (block, hub stream)
+// streams a whole list for one wave of rows.  The rows of G consecutive blocks
+// of one hub stream form one group instead: its list is the union of the G
+// source lists (each a concatenation of whole key frames), a key's mask bits
+// of block b0 + j shifted by n * j (bit f = the group's query frame f).  Pass
+// A scatters every live source entry into a dense per-group mask array over
+// the key rows (atomic OR); pass B compacts each group's array in row order
+// into the group's slot (its capacity, the sum of its sources' sizes, bounds
+// the union), pads it to 64 with mask 0, writes the per-64 mask ANDs and the
+// group's work items.  Key frames stay contiguous in row order, as the
+// backward's derivation requires.
+namespace {
+
+constexpr int kMergeThreads = 1024;
+
+__global__ __launch_bounds__(256) void merge_scatter_kernel(HierMergeArgs a) {
+  const int i = blockIdx.x;                              // source list
+  const int32_t* it = a.items + 8 * (int64_t)a.src_item[i];
+  const int64_t off = it[5];
+  const int cnt = it[6];
+  const int g = a.src_group[i], sh = a.src_shift[i];
+  uint32_t* acc = a.acc + (int64_t)g * a.rows;
+  for (int e = blockIdx.y * blockDim.x + threadIdx.x; e < cnt; e += gridDim.y * blockDim.x) {
+    const uint32_t m = a.kv_mask[off + e];
+    const int k = a.kv_idx[off + e];
+    if (m != 0 && k >= 0 && k < a.rows) atomicOr(&acc[k], m << sh);
+  }
+}
+
+__global__ __launch_bounds__(kMergeThreads) void merge_compact_kernel(HierMergeArgs a) {
+  __shared__ int wsum[kMergeThreads / 64];
+  __shared__ int base_s, first_s;
+  const int g = blockIdx.x;
+  const uint32_t* acc = a.acc + (int64_t)g * a.rows;
+  const int64_t out = a.out_off[g];
+  const int cap = a.out_cap[g];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) {
+    base_s = 0;
+    first_s = -1;
+  }
+  __syncthreads();
+  for (int r0 = 0; r0 < a.rows; r0 += kMergeThreads) {
+    const int r = r0 + threadIdx.x;
+    const uint32_t m = r < a.rows ? acc[r] : 0u;
+    const uint64_t live = __ballot(m != 0);
+    if (lane == 0) wsum[wave] = __popcll(live);
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < kMergeThreads / 64; ++w) {
+      before += w < wave ? wsum[w] : 0;
+      total += wsum[w];
+    }
+    const int pos = base_s + before + __popcll(live & ((1ull << lane) - 1));
+    if (m != 0 && pos < cap) {
+      a.kv_idx[out + pos] = r;
+      a.kv_mask[out + pos] = m;
+    }
+    if (m != 0 && pos == 0) first_s = r;
+    __syncthreads();
+    if (threadIdx.x == 0) base_s += total;
+    __syncthreads();
+  }
+  const int uni = min(base_s, cap);
+  const int padded = min((uni + 63) / 64 * 64, cap);
+  const int pad_idx = first_s < 0 ? 0 : first_s;
+  for (int p = uni + threadIdx.x; p < padded; p += blockDim.x) {
+    a.kv_idx[out + p] = pad_idx;
+    a.kv_mask[out + p] = 0;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < padded / 64; t += blockDim.x) {
+    uint32_t x = ~0u;
+    for (int e = 0; e < 64; ++e) x &= a.kv_mask[out + 64 * t + e];
+    a.blk_and[out / 64 + t] = x;
+  }
+  // the group's items: rows split into rows_per_item pieces
+  const int32_t* d = a.group_desc + 4 * (int64_t)g;      // qbase, qstride, qlen, frames
+  const int rows = d[2] * d[3];
+  const int nit = (rows + a.rows_per_item - 1) / a.rows_per_item;
+  for (int it = threadIdx.x; it < nit; it += blockDim.x) {
+    int32_t* o = a.out_items + 8 * ((int64_t)a.group_item_off[g] + it);
+    o[0] = d[0];
+    o[1] = d[1];
+    o[2] = d[2];
+    o[3] = it * a.rows_per_item;
+    o[4] = min(a.rows_per_item, rows - it * a.rows_per_item);
+    o[5] = (int32_t)out;
+    o[6] = padded;
+    o[7] = d[3];
+  }
+}
+
+}  // namespace
+
+extern "C" int hier_merge_hub_lists(const HierMergeArgs* args, void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
+  const HierMergeArgs& a = *args;
+  HIER_REQUIRE(a.n_groups >= 0 && a.n_src >= 0 && a.rows >= 1 && a.rows_per_item >= 32 &&
+                   a.rows_per_item % 32 == 0 && (int64_t)a.n_groups * a.rows <= (1ll << 31),
+               HIER_EINVAL, "invalid n_groups=%d n_src=%d rows=%d rows_per_item=%d", a.n_groups,
+               a.n_src, a.rows, a.rows_per_item);
+  if (a.n_groups == 0) return HIER_OK;
+  HIER_REQUIRE(a.items && a.kv_idx && a.kv_mask && a.blk_and && a.acc && a.src_item &&
+                   a.src_group && a.src_shift && a.out_off && a.out_cap && a.group_desc &&
+                   a.group_item_off && a.out_items,
+               HIER_EINVAL, "NULL pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t n_acc = (int64_t)a.n_groups * a.rows;
+  hipLaunchKernelGGL(derive_fill_kernel, dim3((unsigned)std::min<int64_t>((n_acc + 255) / 256, 4096)),
+                     dim3(256), 0, s, reinterpret_cast<int32_t*>(a.acc), n_acc, 0);
+  if (a.n_src > 0)
+    hipLaunchKernelGGL(merge_scatter_kernel, dim3(a.n_src, 4), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(merge_compact_kernel, dim3(a.n_groups), dim3(kMergeThreads), 0, s, a);
+  return hier::check_launch("merge kernels");
+}

@@ -38,6 +38,13 @@ ROWS_PER_ITEM = 128     # attention kernel query rows per work item (4 waves x 3
 SEG_ROUND = 64          # hier_segmented_attention.py:371
 TILED_N = 128           # hier_tiled_attention.py:33
 TILED_M = 16            # hier_tiled_attention.py:32
+# temporal blocks whose hub streams share one work group in a full-sequence
+# list: a hub stream has n * KL (or n * KG) rows per block against a key list
+# as long as a member's.  Same-box forward times, per-block / 2 / 4 blocks:
+# C2 2.409 / 2.308 / 2.317 ms, P6 3.626 / 3.514 / 3.543, C3 5.635 / 5.500 /
+# 5.504, P10 7.355 / 7.260 / 7.529 (random per-block groups: the union of four
+# blocks' members is mostly masked), C5 0.700 / 0.698 / 0.696
+MERGE_HUB_BLOCKS = 2
 
 
 def _ceil(a: int, b: int) -> int:
@@ -62,6 +69,8 @@ class TileList:
     # the items' rows are every row of [0, row_extent) exactly once (recorded
     # by the builder from the groups' row descriptors; False = not known)
     rows_exact_cover: bool = False
+    n_groups: int = 0            # groups (items sharing a list); 0 = count from item_ranges
+    merged_blocks: int = 1       # hub streams merged over this many blocks (item_ranges empty)
 
 
 @dataclass(frozen=True)
@@ -446,9 +455,71 @@ def _topo_struct(topo: BlockTopology, dev: torch.device):
     return t, dv
 
 
+class _HubMerge:
+    """The hub-stream merge of a full-sequence tile list (``hier_merge_hub_lists``):
+    host plan and device arrays, replayable on new lists of the same layout."""
+
+    def __init__(self, topo: BlockTopology, G: int, tile_h, tile_off, item_start, n_keys: int,
+                 n_items: int, rows_per_item: int, row_extent: int, dev):
+        P, N, n, B = topo.P, topo.N, topo.n_frames, topo.B
+        hubs = ([] if topo.no_local else list(range(P, P + N))) + [P + N]
+        src_item, src_group, src_shift, caps, desc, nits = [], [], [], [], [], []
+        for s in hubs:
+            ql = _qlen(topo, s)
+            if ql <= 0:
+                continue
+            kind = 1 if s < P + N else 2
+            for b0 in range(0, B, G):
+                blocks = list(range(b0, min(B, b0 + G)))
+                g = len(caps)
+                for b in blocks:
+                    src_item.append(int(item_start[b, s]))
+                    src_group.append(g)
+                    src_shift.append(n * (b - b0))
+                caps.append(int(sum(int(tile_h[b, s]) for b in blocks)))
+                frames = n * len(blocks)
+                desc.append([int(topo.tile_qbase[b0][s]), int(topo.tile_qstride[kind]), ql, frames])
+                nits.append(-(-ql * frames // rows_per_item))
+        self.n_groups = len(caps)
+        self.n_items = int(sum(nits))
+        off = n_keys + np.concatenate([[0], np.cumsum(caps)]).astype(np.int64)
+        self.capacity = int(off[-1])
+        self.first_player = int(item_start[0, 0])
+        self.frames = n * G
+        i32 = lambda a: torch.tensor(np.asarray(a, np.int32).reshape(-1), device=dev)
+        self._dev = dict(src_item=i32(src_item), src_group=i32(src_group), src_shift=i32(src_shift),
+                         out_off=torch.tensor(off[:-1], dtype=torch.int64, device=dev),
+                         out_cap=i32(caps), group_desc=i32(desc),
+                         group_item_off=i32(np.concatenate([[0], np.cumsum(nits)])[:-1]))
+        self.acc = torch.empty((max(self.n_groups, 1), row_extent), dtype=torch.int32, device=dev)
+        self.n_src, self.rows, self.rpi = len(src_item), row_extent, rows_per_item
+
+    def run(self, items, kv_idx, kv_mask, blk_and, n_items: int, stream) -> torch.Tensor:
+        """Merged lists into their slots; the final items (merged hub groups,
+        then the players' items of the built list)."""
+        out = torch.empty((max(self.n_items, 1), 8), dtype=torch.int32, device=items.device)
+        d = self._dev
+        a = _capi.HierMergeArgs(
+            n_groups=self.n_groups, n_src=self.n_src, rows=self.rows, rows_per_item=self.rpi,
+            items=items.data_ptr(), kv_idx=kv_idx.data_ptr(), kv_mask=kv_mask.data_ptr(),
+            blk_and=blk_and.data_ptr(), acc=self.acc.data_ptr(),
+            **{k: v.data_ptr() for k, v in d.items()}, out_items=out.data_ptr())
+        _capi.call("hier_merge_hub_lists", C.byref(a), stream)
+        return torch.cat([out[:self.n_items], items[self.first_player:n_items]])
+
+
 def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
-          tiled: bool = False, rows_per_item: int = ROWS_PER_ITEM) -> BuildResult:
-    """Run the two device passes and return device tensors."""
+          tiled: bool = False, rows_per_item: int = ROWS_PER_ITEM,
+          merge_hubs: Optional[int] = None) -> BuildResult:
+    """Run the two device passes and return device tensors.  With
+    ``merge_hubs = G >= 2`` (full-sequence topologies), the hub streams of G
+    consecutive temporal blocks share one work group (``_HubMerge``).  The
+    default merges four blocks for full-sequence topologies when no
+    reference-format arrays are requested (those callers may launch subsets
+    of blocks through ``item_ranges``, which a merged list does not keep)."""
+    if merge_hubs is None:
+        merge_hubs = MERGE_HUB_BLOCKS if (topo.frames_valid and not tiled and
+                                          segmented_block_m is None) else 0
     topo.validate()
     dev = torch.device(device)
     if dev.type != "cuda":
@@ -499,9 +570,15 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
         item_start[b, s] = cursor
         cursor += int(nit[b, s])
     n_items = cursor
-    kv_idx = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
-    kv_mask = torch.empty(max(n_keys, 1), dtype=torch.int32, device=dev)
-    blk_and = torch.empty(max(n_keys // TILE_KEYS, 1), dtype=torch.int32, device=dev)
+    merge = None
+    G = min(int(merge_hubs), 32 // n) if merge_hubs else 0
+    if G >= 2 and topo.frames_valid and B >= 2:
+        merge = _HubMerge(topo, G, tile_h, tile_off, item_start, n_keys, n_items, rows_per_item,
+                          group_rows_cover(topo)[0], dev)
+    cap = merge.capacity if merge is not None else n_keys
+    kv_idx = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    kv_mask = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    blk_and = torch.empty(max(cap // TILE_KEYS, 1), dtype=torch.int32, device=dev)
     items = torch.empty((max(n_items, 1), 8), dtype=torch.int32, device=dev)
     dbuf(tile_off[:-1], np.int64, "tile_kv_off")
     dbuf(item_start.reshape(-1), np.int32, "tile_item_off")
@@ -585,11 +662,24 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
             if flat and w > 0:
                 key_ext = max(key_ext, max(flat) + w)
     row_ext, exact = group_rows_cover(topo)
-    tiles = TileList(items=items[:n_items], kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
-                     n_items=n_items, item_ranges=ranges, logical_pairs=int(pairs.sum()),
-                     key_extent=int(key_ext), row_extent=int(row_ext),
-                     rows_per_item=rows_per_item, frames_per_group=int(n),
-                     rows_exact_cover=exact)
+    if merge is not None:
+        final = merge.run(items, kv_idx, kv_mask, blk_and, n_items, stream)
+        n_player = n_items - merge.first_player
+        tiles = TileList(items=final, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
+                         n_items=int(final.shape[0]), item_ranges=(),
+                         logical_pairs=int(pairs.sum()), key_extent=int(key_ext),
+                         row_extent=int(row_ext), rows_per_item=rows_per_item,
+                         frames_per_group=merge.frames, rows_exact_cover=exact,
+                         n_groups=merge.n_groups + P * B, merged_blocks=G)
+        tiles._merge = merge
+        tiles._prebuild_items = n_items
+        assert tiles.n_items == merge.n_items + n_player
+    else:
+        tiles = TileList(items=items[:n_items], kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
+                         n_items=n_items, item_ranges=ranges, logical_pairs=int(pairs.sum()),
+                         key_extent=int(key_ext), row_extent=int(row_ext),
+                         rows_per_item=rows_per_item, frames_per_group=int(n),
+                         rows_exact_cover=exact)
     tiles._keepalive = (dv, keep)  # device inputs must outlive the async build
     tiles._layout = (tile_off[:-1].copy(), item_start.reshape(-1).copy())   # per (block, stream)
     layouts = None
@@ -707,7 +797,9 @@ def transpose_tiles_host(tiles: TileList) -> TileList:
                    kv_idx=to_dev(q_idx), kv_mask=to_dev(q_mask), blk_and=to_dev(blk_and),
                    n_items=tiles.n_items, item_ranges=tiles.item_ranges,
                    logical_pairs=pairs, key_extent=tiles.row_extent, row_extent=tiles.key_extent,
-                   rows_per_item=tiles.rows_per_item, rows_exact_cover=tiles.rows_exact_cover)
+                   rows_per_item=tiles.rows_per_item, rows_exact_cover=tiles.rows_exact_cover,
+                   n_groups=tiles.n_groups, frames_per_group=tiles.frames_per_group,
+                   merged_blocks=tiles.merged_blocks)
     return out
 
 
@@ -849,6 +941,8 @@ _DERIVE_ERRORS = ((1, "a token is a query row of two groups"),
 
 
 def _groups_and_frames(tiles: TileList):
+    if tiles.n_groups and tiles.frames_per_group:
+        return int(tiles.n_groups), int(tiles.frames_per_group)
     if tiles.item_ranges and tiles.frames_per_group:
         return sum(len(b) for b in tiles.item_ranges), int(tiles.frames_per_group)
     it = tiles.items[:tiles.n_items].cpu().numpy()
@@ -896,7 +990,9 @@ def _derive_device(tiles: TileList, ste_geometry):
     kt = TileList(items=k_items, kv_idx=k_idx, kv_mask=k_mask, blk_and=k_blk,
                   n_items=tiles.n_items, item_ranges=tiles.item_ranges, logical_pairs=pairs,
                   key_extent=tiles.row_extent, row_extent=tiles.key_extent,
-                  rows_per_item=tiles.rows_per_item, rows_exact_cover=tiles.rows_exact_cover)
+                  rows_per_item=tiles.rows_per_item, rows_exact_cover=tiles.rows_exact_cover,
+                  n_groups=tiles.n_groups, frames_per_group=tiles.frames_per_group,
+                  merged_blocks=tiles.merged_blocks)
     ste = None
     if n_ste_items > 0:
         lst = TileList(items=s_items, kv_idx=s_idx, kv_mask=s_mask, blk_and=s_blk,
@@ -1023,6 +1119,26 @@ def build_hier_tiled_full_sequence_layouts(*, device, num_players, num_frames, n
     P, T, L = int(num_players), int(num_frames), int(num_patches)
     N, KL, KG = int(num_groups), int(num_local_hub_tokens), int(num_global_hub_tokens)
     n, window = int(num_frame_per_block), int(local_attn_size)
+    labels, active = tiled_full_sequence_inputs(
+        num_players=P, num_frames=T, num_groups=N, num_frame_per_block=n,
+        local_attn_size=window, group_labels=group_labels, active_group=active_group)
+    key = ("full", str(torch.device(device)), P, T, L, N, KL, KG, n, window, labels.tobytes(),
+           active.tobytes(), bool(direct_player), TILED_M, TILED_N)
+    hit = _lru_get(_LAYOUT_CACHE, key)
+    if hit is None:
+        topo = full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=window,
+                                      direct=direct_player, labels=labels, active=active)
+        hit = tuple(build(topo, device, tiled=True).tiled)
+        _lru_put(_LAYOUT_CACHE, key, hit, "WAN_HIER_TILED_LAYOUT_CACHE_SIZE", "2")
+    return hit
+
+
+def tiled_full_sequence_inputs(*, num_players, num_frames, num_groups, num_frame_per_block,
+                               local_attn_size, group_labels, active_group):
+    """The reference's checks of a full-sequence labels topology
+    (hier_tiled_attention.py:244-285): ``(labels, active)`` as host arrays."""
+    P, T, N = int(num_players), int(num_frames), int(num_groups)
+    n, window = int(num_frame_per_block), int(local_attn_size)
     if T % n != 0:
         raise ValueError(f"Tiled128 requires T % n == 0, got T={T}, n={n}")
     if window != -1 and window < n:
@@ -1037,15 +1153,7 @@ def build_hier_tiled_full_sequence_layouts(*, device, num_players, num_frames, n
     for s in range(0, T, n):
         if any(not np.array_equal(labels[t], labels[s]) for t in range(s + 1, min(s + n, T))):
             raise ValueError("Tiled128 requires group labels constant inside each temporal block")
-    key = ("full", str(torch.device(device)), P, T, L, N, KL, KG, n, window, labels.tobytes(),
-           active.tobytes(), bool(direct_player), TILED_M, TILED_N)
-    hit = _lru_get(_LAYOUT_CACHE, key)
-    if hit is None:
-        topo = full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=window,
-                                      direct=direct_player, labels=labels, active=active)
-        hit = tuple(build(topo, device, tiled=True).tiled)
-        _lru_put(_LAYOUT_CACHE, key, hit, "WAN_HIER_TILED_LAYOUT_CACHE_SIZE", "2")
-    return hit
+    return labels, active
 
 
 def full_sequence_tiles(*, device, P, T, L, N, KL, KG, n, window, direct, labels=None, active=None,
@@ -1155,7 +1263,9 @@ class MembershipLogitsPlan:
         _capi.call("hier_membership_from_logits", C.byref(self._margs), stream)
         sup = self.sup
         i32 = dict(dtype=torch.int32, device=dev)
-        items = torch.empty((sup.n_items, 8), **i32)
+        merge = getattr(sup, "_merge", None)
+        n_pre = sup._prebuild_items if merge is not None else sup.n_items
+        items = torch.empty((n_pre, 8), **i32)
         kv_idx = torch.empty(self.n_keys, **i32)
         kv_mask = torch.empty(self.n_keys, **i32)
         blk = torch.empty(max(self.n_keys // TILE_KEYS, 1), **i32)
@@ -1165,11 +1275,14 @@ class MembershipLogitsPlan:
         out.tile_kv_idx, out.tile_kv_mask = kv_idx.data_ptr(), kv_mask.data_ptr()
         out.tile_blk_and, out.tile_items = blk.data_ptr(), items.data_ptr()
         _capi.call("hier_meta_build", C.byref(self.t), C.byref(out), stream)
+        if merge is not None:
+            items = merge.run(items, kv_idx, kv_mask, blk, n_pre, stream)
         tiles = TileList(items=items, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk,
                          n_items=sup.n_items, item_ranges=sup.item_ranges, logical_pairs=-1,
                          key_extent=sup.key_extent, row_extent=sup.row_extent,
                          rows_per_item=sup.rows_per_item, frames_per_group=sup.frames_per_group,
-                         rows_exact_cover=sup.rows_exact_cover)
+                         rows_exact_cover=sup.rows_exact_cover, n_groups=sup.n_groups,
+                         merged_blocks=sup.merged_blocks)
         # key-major list, sized by the superset's
         a = self._derive_args(tiles)
         a.ws, a.ws_bytes, a.totals = self.ws.data_ptr(), int(self.ws.numel()), self.totals.data_ptr()
@@ -1185,7 +1298,9 @@ class MembershipLogitsPlan:
         kt = TileList(items=k_items, kv_idx=k_idx, kv_mask=k_mask, blk_and=k_blk,
                       n_items=sup.n_items, item_ranges=sup.item_ranges, logical_pairs=-1,
                       key_extent=sup.row_extent, row_extent=sup.key_extent,
-                      rows_per_item=sup.rows_per_item, rows_exact_cover=sup.rows_exact_cover)
+                      rows_per_item=sup.rows_per_item, rows_exact_cover=sup.rows_exact_cover,
+                      n_groups=sup.n_groups, frames_per_group=sup.frames_per_group,
+                      merged_blocks=sup.merged_blocks)
         tiles.__dict__["_derived"] = {None: (kt, None)}
         tiles._keepalive = (self, a, lg)
         return tiles

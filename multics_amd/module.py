@@ -249,13 +249,19 @@ class SelfAttention(nn.Module):
         """Full-sequence hierarchical attention (labels topology), reference
         signature (attention.py:367-434)."""
         if tiled_layouts is None:
-            tiled_layouts = M.build_hier_tiled_full_sequence_layouts(
-                device=x.device, num_players=num_players, num_frames=num_frames,
-                num_patches=num_patches, num_groups=num_groups,
-                num_local_hub_tokens=num_local_hub_tokens,
-                num_global_hub_tokens=num_global_hub_tokens,
-                num_frame_per_block=self.num_frame_per_block, local_attn_size=self.local_attn_size,
-                group_labels=group_labels, active_group=active_group, direct_player=direct_player)
+            # the module needs only the HIP tile list (merged hub groups):
+            # no reference-format layouts are built
+            labels, active = M.tiled_full_sequence_inputs(
+                num_players=num_players, num_frames=num_frames, num_groups=num_groups,
+                num_frame_per_block=self.num_frame_per_block,
+                local_attn_size=self.local_attn_size, group_labels=group_labels,
+                active_group=active_group)
+            tiles = M.full_sequence_tiles(
+                device=x.device, P=int(num_players), T=int(num_frames), L=int(num_patches),
+                N=int(num_groups), KL=int(num_local_hub_tokens), KG=int(num_global_hub_tokens),
+                n=self.num_frame_per_block, window=self.local_attn_size,
+                direct=bool(direct_player), labels=labels, active=active)
+            return self._hier(x, freqs, tiles, cam_tokens)
         tiles = tiled_layouts[0].tiles
         if tiles is None or any(l.tiles is not tiles for l in tiled_layouts):
             raise ValueError("tiled_layouts must come from one build_hier_tiled_full_sequence_layouts call")

@@ -27,6 +27,7 @@ STRUCTS = {
     "HierSteReduceArgs": _capi.HierSteReduceArgs,
     "HierMembershipArgs": _capi.HierMembershipArgs,
     "HierPrologueBwdArgs": _capi.HierPrologueBwdArgs,
+    "HierMergeArgs": _capi.HierMergeArgs,
 }
 
 

@@ -159,3 +159,58 @@ def test_varlen_plan_on_device_arrays(name):
         assert got[k] == want[k], k
     assert M._get_varlen_plan(kv_index=kv, kv_count=kc, qbase=qb, qlen=nq, seg_ids=sg,
                               query_tokens=qt) is got
+
+
+def _row_owner(tiles):
+    """{token: (item row index r, item)} over every item, and the token list."""
+    it = tiles.items[:tiles.n_items].cpu().numpy()
+    owner = {}
+    for k, (qb, qs, ql, r0, rc, off, cnt, nf) in enumerate(it):
+        for r in range(r0, r0 + rc):
+            j, i = divmod(r, ql)
+            tok = qb + j * qs + i
+            assert tok not in owner, tok
+            owner[tok] = (j, k)
+    return owner, it
+
+
+def _keys_of(tiles, it, idx, msk, owner, tok):
+    j, k = owner[tok]
+    off, cnt = it[k, 5], it[k, 6]
+    sel = ((msk[off:off + cnt] >> j) & 1) == 1
+    return set(idx[off:off + cnt][sel].tolist())
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c3", "p10", "c5"])
+def test_merged_hub_groups_keep_every_key_set(cfg):
+    """Hub streams merged across temporal blocks (two by default for
+    full-sequence lists; four here, the widest masks) against the per-block
+    list of the same topology:
+    every row owned once, every sampled row's key set equal (players, local
+    hubs and global rows of the first, middle and last blocks, random rows),
+    the same pair count; hub groups span up to 12 query frames, their lists
+    in key-row order."""
+    need_gpu()
+    from tests.test_gpu_fullsize import _case, _rows
+    say("merged hub groups", cfg)
+    meta, topo, _ = _case(cfg)
+    assert M.build(meta, "cuda").tiles.merged_blocks == M.MERGE_HUB_BLOCKS
+    merged = M.build(meta, "cuda", merge_hubs=4).tiles
+    plain = M.build(meta, "cuda", merge_hubs=0).tiles
+    assert merged.merged_blocks == 4 and plain.merged_blocks == 1
+    assert merged.n_items < plain.n_items
+    assert merged.logical_pairs == plain.logical_pairs and merged.rows_exact_cover
+    own_m, it_m = _row_owner(merged)
+    own_p, it_p = _row_owner(plain)
+    assert sorted(own_m) == list(range(topo.S)) and own_m.keys() == own_p.keys()
+    idx_m, msk_m = merged.kv_idx.cpu().numpy(), merged.kv_mask.cpu().numpy().view(np.uint32)
+    idx_p, msk_p = plain.kv_idx.cpu().numpy(), plain.kv_mask.cpu().numpy().view(np.uint32)
+    for r in _rows(topo, np.random.default_rng(1), n_random=256):
+        assert _keys_of(merged, it_m, idx_m, msk_m, own_m, int(r)) == \
+            _keys_of(plain, it_p, idx_p, msk_p, own_p, int(r)), (cfg, r)
+    a0 = topo.P * topo.T * topo.L
+    hub = it_m[it_m[:, 0] >= a0]
+    assert (hub[:, 7] <= 12).all() and (hub[:, 7] == 12).any()
+    for qb, qs, ql, r0, rc, off, cnt, nf in hub:
+        live = idx_m[off:off + cnt][msk_m[off:off + cnt] != 0]
+        assert (np.diff(live) > 0).all()
