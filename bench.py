@@ -631,6 +631,21 @@ def bench_action_temporal(dev, passes=20):
             "max_abs_vs_sdpa": round(diff, 5)}
 
 
+# the suite of the default run, in its order: name -> fn(dev[, steps, warmup])
+SUITES = {
+    "fwd_p6": lambda dev, *a: bench_forward_cfg("p6", dev, *a),
+    "fwd_c3": lambda dev, *a: bench_forward_cfg("c3", dev, *a),
+    "fwd_p10": lambda dev, *a: bench_forward_cfg("p10", dev, *a),
+    "layer_c2": bench_layer,
+    "block_tail_c2": bench_block_tail,
+    "training_c5": bench_training,
+    "module_training_c5": bench_module_training,
+    "rollout_c4": lambda dev, *a: bench_rollout(dev, *a[:1]),
+    "rollout_c4_cfg": lambda dev, *a: bench_rollout_cfg(dev, *a[:1]),
+    "action_temporal_c4": lambda dev, *a: bench_action_temporal(dev, *a[:1]),
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -643,6 +658,8 @@ def main():
                     help="skip the other configurations (6/8/10 players, training, rollout)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device copy (HBM counter calibration)")
+    ap.add_argument("--only", choices=sorted(SUITES),
+                    help="run one entry of the suite alone and print its line (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the hierarchical attention of one layer shards by "
@@ -654,6 +671,10 @@ def main():
         sys.exit(1)
     from multics_amd.kernels import hier_attention_forward, qkv_prologue
     dev = torch.device("cuda", 0)
+    if args.only:
+        res = SUITES[args.only](dev, max(args.steps, 1), args.warmup)
+        print(json.dumps({"suite": args.only, **res}), flush=True)
+        return
     P, T, L, N, KL, KG, n, W, H, D, grp = CONFIGS[args.config]
     topo, tiles, host_build_s, topo_args = build_case(args.config, dev)
     S = P * T * L + T * (N * KL + KG)
@@ -740,20 +761,13 @@ def main():
                      "traffic": profiled_traffic(args.config)},
         "cpu_baseline": cpu,
         "extra": {"metadata_build_ms": round(float(np.median(meta_ms)), 3),
-                  "prologue_ms": round(pro_ms, 4), "work_items": tiles.n_items * H},
+                  "prologue_ms": round(pro_ms, 4), "work_items": (tiles.fwd_n_items or tiles.n_items) * H},
     }
     if not args.no_suite:
         suite = {}
-        for cfg in ("p6", "c3", "p10"):
-            if cfg != args.config:
-                suite[f"fwd_{cfg}"] = bench_forward_cfg(cfg, dev)
-        suite["layer_c2"] = bench_layer(dev)
-        suite["block_tail_c2"] = bench_block_tail(dev)
-        suite["training_c5"] = bench_training(dev)
-        suite["module_training_c5"] = bench_module_training(dev)
-        suite["rollout_c4"] = bench_rollout(dev)
-        suite["rollout_c4_cfg"] = bench_rollout_cfg(dev)
-        suite["action_temporal_c4"] = bench_action_temporal(dev)
+        for name, fn in SUITES.items():
+            if name != f"fwd_{args.config}":
+                suite[name] = fn(dev)
         line["extra"]["suite"] = suite
     print(json.dumps(line), flush=True)
 

@@ -214,6 +214,14 @@ typedef struct HierMergeArgs {
   const int32_t* group_desc;       /* [n_groups][4] qbase, qstride, qlen, frames */
   const int32_t* group_item_off;   /* [n_groups] first output item             */
   int32_t* out_items;              /* [sum items][8]                           */
+  /* Optional per-source bit selection (both NULL: every source's whole     */
+  /* mask): source i contributes bits [src_from[i], src_from[i] +           */
+  /* src_nbits[i]) of its masks, moved down to bit 0 before the shift, so a  */
+  /* player's last query frames can join a hub group under bits of their    */
+  /* own (its group's items then take their rows from a row table: qstride  */
+  /* -1 in group_desc).                                                     */
+  const int32_t* src_from;         /* [n_src] first mask bit taken             */
+  const int32_t* src_nbits;        /* [n_src] number of bits taken (1..32)     */
 } HierMergeArgs;
 
 int hier_merge_hub_lists(const HierMergeArgs* args, void* stream);
@@ -330,6 +338,11 @@ typedef struct HierFwdArgs {
   const int32_t* tile_kv_idx;
   const uint32_t* tile_kv_mask;
   const uint32_t* tile_blk_and;
+  /* Items whose qstride is -1 take their rows from this table instead:     */
+  /* row r of such an item is the pair (token, mask bit) at                 */
+  /* row_table[2 * (qbase + r)] (r = row_start ..), so one item can hold rows */
+  /* of several streams against one key list.  NULL if no item does.        */
+  const int32_t* row_table;
 } HierFwdArgs;
 
 int hier_attn_fwd(const HierFwdArgs* args, void* stream);

@@ -70,7 +70,8 @@ class HierFwdArgs(C.Structure):
                [(n, vp) for n in ("q", "k", "v", "o", "lse")] + \
                [(n, i64) for n in ("q_ss", "q_sh", "k_ss", "k_sh", "v_ss", "v_sh", "o_ss", "o_sh",
                                    "lse_stride_h")] + \
-               [(n, vp) for n in ("tile_items", "tile_kv_idx", "tile_kv_mask", "tile_blk_and")]
+               [(n, vp) for n in ("tile_items", "tile_kv_idx", "tile_kv_mask", "tile_blk_and",
+                                  "row_table")]
 
 
 class HierBwdArgs(C.Structure):
@@ -145,7 +146,7 @@ class HierMergeArgs(C.Structure):
     _fields_ = [(n, i32) for n in ("n_groups", "n_src", "rows", "rows_per_item")] + \
                [(n, vp) for n in ("items", "kv_idx", "kv_mask", "blk_and", "acc", "src_item",
                                   "src_group", "src_shift", "out_off", "out_cap", "group_desc",
-                                  "group_item_off", "out_items")]
+                                  "group_item_off", "out_items", "src_from", "src_nbits")]
 
 
 EXPORTS = {

@@ -88,8 +88,15 @@ __device__ __forceinline__ void rows_init(Rows<D>& R, const HierFwdArgs& a, cons
   const int r = rrel + (lane & 31);
   R.valid = r < row_count;
   const int ri = row_start + (R.valid ? r : 0);
-  R.qframe = ri / qlen;
-  R.qtok = qbase + R.qframe * qstride + (ri - R.qframe * qlen);
+  if (qstride < 0) {            // rows from the row table: (token, mask bit) pairs
+    R.valid = R.valid && a.row_table != nullptr;   // no table: the item has no rows
+    const int2 tb = R.valid ? reinterpret_cast<const int2*>(a.row_table)[qbase + ri] : int2{0, 0};
+    R.qtok = tb.x;
+    R.qframe = tb.y;
+  } else {
+    R.qframe = ri / qlen;
+    R.qtok = qbase + R.qframe * qstride + (ri - R.qframe * qlen);
+  }
   R.bits = wave_or(R.valid ? (1u << R.qframe) : 0u);
   const uint16_t* qp = a.q + (int64_t)R.qtok * a.q_ss + (int64_t)head * a.q_sh + 8 * (lane >> 5);
 #pragma unroll

@@ -1360,6 +1360,14 @@ extern "C" int hier_membership_from_logits(const HierMembershipArgs* args, void*
 // the union), pads it to 64 with mask 0, writes the per-64 mask ANDs and the
 // group's work items.  Key frames stay contiguous in row order, as the
 // backward's derivation requires.
+//
+// A forward-only group may also take the ragged last item of the players
+// that belong to its hub: that item has a few rows (n * L mod 128) but walks
+// the player's whole list, and a member's keys are a subset of its hub's, so
+// its rows join the hub's items at no extra key.  Such a source contributes
+// only the bits of its rows' query frames (src_from / src_nbits), shifted to
+// bits of their own; the group's items then read their (token, bit) rows
+// from a row table.
 namespace {
 
 constexpr int kMergeThreads = 1024;
@@ -1370,9 +1378,16 @@ __global__ __launch_bounds__(256) void merge_scatter_kernel(HierMergeArgs a) {
   const int64_t off = it[5];
   const int cnt = it[6];
   const int g = a.src_group[i], sh = a.src_shift[i];
+  int from = 0;
+  uint32_t keep = ~0u;
+  if (a.src_from != nullptr) {
+    from = a.src_from[i] & 31;
+    const int nb = a.src_nbits[i];
+    keep = nb >= 32 ? ~0u : (nb <= 0 ? 0u : (1u << nb) - 1u);
+  }
   uint32_t* acc = a.acc + (int64_t)g * a.rows;
   for (int e = blockIdx.y * blockDim.x + threadIdx.x; e < cnt; e += gridDim.y * blockDim.x) {
-    const uint32_t m = a.kv_mask[off + e];
+    const uint32_t m = (a.kv_mask[off + e] >> from) & keep;
     const int k = a.kv_idx[off + e];
     if (m != 0 && k >= 0 && k < a.rows) atomicOr(&acc[k], m << sh);
   }
@@ -1457,6 +1472,8 @@ extern "C" int hier_merge_hub_lists(const HierMergeArgs* args, void* stream) {
                    a.src_group && a.src_shift && a.out_off && a.out_cap && a.group_desc &&
                    a.group_item_off && a.out_items,
                HIER_EINVAL, "NULL pointer");
+  HIER_REQUIRE((a.src_from == nullptr) == (a.src_nbits == nullptr), HIER_EINVAL,
+               "src_from and src_nbits must both be set or both be NULL");
   hipStream_t s = (hipStream_t)stream;
   const int64_t n_acc = (int64_t)a.n_groups * a.rows;
   hipLaunchKernelGGL(derive_fill_kernel, dim3((unsigned)std::min<int64_t>((n_acc + 255) / 256, 4096)),

@@ -46,6 +46,9 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
     ``q`` / ``out`` rows are addressed by the tile list's query rows, ``k`` / ``v``
     rows by its key indices; all are bf16 with a unit-stride head dimension.
     ``lse`` (optional, fp32 [H, S_q]) receives the natural-log softmax normaliser.
+    Without ``item_range``, a list that carries the forward's own items
+    (``TileList.fwd_items``: the players' ragged last items folded into their
+    hubs' groups) runs those.
     """
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
         if t.dtype != torch.bfloat16:
@@ -70,7 +73,10 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
     if lse is not None and (lse.dtype != torch.float32 or lse.dim() != 2 or lse.shape[0] != H
                             or lse.shape[1] < tiles.row_extent or lse.stride(1) != 1):
         raise ValueError("lse must be fp32 [H, >=rows] with unit row stride")
+    items, row_table = tiles.items, None
     first, last = item_range if item_range is not None else (0, tiles.n_items)
+    if item_range is None and tiles.fwd_items is not None:
+        items, row_table, last = tiles.fwd_items, tiles.row_table, tiles.fwd_n_items
     if last <= first:
         return out
     args = _capi.HierFwdArgs(
@@ -80,8 +86,9 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
         lse=None if lse is None else lse.data_ptr(),
         q_ss=q_ss, q_sh=q_sh, k_ss=k_ss, k_sh=k_sh, v_ss=v_ss, v_sh=v_sh, o_ss=o_ss, o_sh=o_sh,
         lse_stride_h=0 if lse is None else lse.stride(0),
-        tile_items=tiles.items.data_ptr() + first * 8 * 4, tile_kv_idx=tiles.kv_idx.data_ptr(),
-        tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr())
+        tile_items=items.data_ptr() + first * 8 * 4, tile_kv_idx=tiles.kv_idx.data_ptr(),
+        tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr(),
+        row_table=None if row_table is None else row_table.data_ptr())
     _capi.call("hier_attn_fwd", C.byref(args), _stream(q.device))
     return out
 

@@ -71,6 +71,13 @@ class TileList:
     rows_exact_cover: bool = False
     n_groups: int = 0            # groups (items sharing a list); 0 = count from item_ranges
     merged_blocks: int = 1       # hub streams merged over this many blocks (item_ranges empty)
+    # The forward's own items (None: ``items``): the players' ragged last items
+    # folded into their local hubs' groups, whose items (qstride -1) take
+    # their rows from ``row_table`` ([rows, 2] int32 token, mask bit).  The
+    # backward and the key-major derivation use ``items``.
+    fwd_items: Optional[torch.Tensor] = None
+    fwd_n_items: int = 0
+    row_table: Optional[torch.Tensor] = None
 
 
 @dataclass(frozen=True)
@@ -455,15 +462,43 @@ def _topo_struct(topo: BlockTopology, dev: torch.device):
     return t, dv
 
 
+def _member(topo: BlockTopology, b: int, f: int, g: int, p: int) -> bool:
+    """Whether player p belongs to group slot g at query frame f of block b."""
+    if topo.membership is not None:
+        return bool(topo.membership[topo.q_frames[b][f], g, p])
+    if topo.labels is not None:
+        return int(topo.labels[b][f][p]) == g
+    return False
+
+
 class _HubMerge:
     """The hub-stream merge of a full-sequence tile list (``hier_merge_hub_lists``):
-    host plan and device arrays, replayable on new lists of the same layout."""
+    host plan and device arrays, replayable on new lists of the same layout.
+
+    With ``fold_tails`` the merge also writes a forward-only list: each local
+    hub group may take the ragged last item of the players that belong to its
+    hub in the rows' frames (a member's keys are a subset of its hub's, so the
+    group's key list does not grow), as long as the group's rows fit the
+    items it has anyway and its masks have bits left.  Those rows get mask
+    bits of their own above the hub's frames and are addressed through a row
+    table of (token, bit) pairs.  The backward keeps the list without them."""
 
     def __init__(self, topo: BlockTopology, G: int, tile_h, tile_off, item_start, n_keys: int,
-                 n_items: int, rows_per_item: int, row_extent: int, dev):
+                 n_items: int, rows_per_item: int, row_extent: int, dev, fold_tails: bool = False):
         P, N, n, B = topo.P, topo.N, topo.n_frames, topo.B
+        rpi = rows_per_item
         hubs = ([] if topo.no_local else list(range(P, P + N))) + [P + N]
-        src_item, src_group, src_shift, caps, desc, nits = [], [], [], [], [], []
+        src_item, src_group, src_shift, src_from, src_nbits = [], [], [], [], []
+        caps, desc, nits, group_srcs = [], [], [], []
+
+        def add_source(item, group, shift, first_bit=0, nbits=32):
+            src_item.append(int(item))
+            src_group.append(group)
+            src_shift.append(int(shift))
+            src_from.append(int(first_bit))
+            src_nbits.append(int(nbits))
+
+        local_groups = []            # (group, hub stream, blocks)
         for s in hubs:
             ql = _qlen(topo, s)
             if ql <= 0:
@@ -473,50 +508,131 @@ class _HubMerge:
                 blocks = list(range(b0, min(B, b0 + G)))
                 g = len(caps)
                 for b in blocks:
-                    src_item.append(int(item_start[b, s]))
-                    src_group.append(g)
-                    src_shift.append(n * (b - b0))
+                    add_source(item_start[b, s], g, n * (b - b0))
                 caps.append(int(sum(int(tile_h[b, s]) for b in blocks)))
                 frames = n * len(blocks)
                 desc.append([int(topo.tile_qbase[b0][s]), int(topo.tile_qstride[kind]), ql, frames])
-                nits.append(-(-ql * frames // rows_per_item))
-        self.n_groups = len(caps)
+                nits.append(-(-ql * frames // rpi))
+                if kind == 1:
+                    local_groups.append((g, s, blocks))
+        self.n_groups = len(caps)                     # groups of the shared list
         self.n_items = int(sum(nits))
+        # ---- forward-only groups: local hubs with their members' last items
+        rows_tab, fwd_groups, taken = [], [], set()
+        if fold_tails:
+            ql_p = topo.L
+            rows_p = n * ql_p
+            n_it_p = -(-rows_p // rpi)
+            r0 = (n_it_p - 1) * rpi
+            tail_rows = rows_p - r0
+            f0, f1 = r0 // ql_p, (rows_p - 1) // ql_p
+            nb = f1 - f0 + 1
+            if ql_p > 0 and tail_rows < rpi:
+                for g, s, blocks in local_groups:
+                    ql, frames = desc[g][2], desc[g][3]
+                    hub_rows = ql * frames
+                    room = max(1, -(-hub_rows // rpi)) * rpi - hub_rows
+                    bits = frames
+                    tails = []
+                    for b in blocks:
+                        for p in range(P):
+                            if ((b, p) in taken or tail_rows > room or bits + nb > 32
+                                    or int(tile_h[b, p]) == 0):
+                                continue
+                            if all(_member(topo, b, f, s - P, p) for f in range(f0, f1 + 1)):
+                                tails.append((b, p, bits))
+                                taken.add((b, p))
+                                room -= tail_rows
+                                bits += nb
+                    if not tails:
+                        continue
+                    fg = len(caps)
+                    for i in range(len(src_item)):
+                        if src_group[i] == g:
+                            add_source(src_item[i], fg, src_shift[i])
+                    table_off = len(rows_tab)
+                    qb, qs = desc[g][0], desc[g][1]
+                    for r in range(hub_rows):
+                        f = r // ql
+                        rows_tab.append((qb + f * qs + r - f * ql, f))
+                    cap = caps[g]
+                    for b, p, bit in tails:
+                        add_source(item_start[b, p], fg, bit, f0, nb)
+                        cap += int(tile_h[b, p])
+                        pb, ps = int(topo.tile_qbase[b][p]), int(topo.tile_qstride[0])
+                        for r in range(r0, rows_p):
+                            f = r // ql_p
+                            rows_tab.append((pb + f * ps + r - f * ql_p, bit + f - f0))
+                    n_rows = len(rows_tab) - table_off
+                    caps.append(cap)
+                    desc.append([table_off, -1, 1, n_rows])
+                    nits.append(-(-n_rows // rpi))
+                    fwd_groups.append(g)
+        self.n_all_groups = len(caps)
+        item_off = np.concatenate([[0], np.cumsum(nits)]).astype(np.int64)
+        self.n_out_items = int(item_off[-1])
         off = n_keys + np.concatenate([[0], np.cumsum(caps)]).astype(np.int64)
         self.capacity = int(off[-1])
         self.first_player = int(item_start[0, 0])
         self.frames = n * G
+        self.folded_tails = len(taken)
         i32 = lambda a: torch.tensor(np.asarray(a, np.int32).reshape(-1), device=dev)
         self._dev = dict(src_item=i32(src_item), src_group=i32(src_group), src_shift=i32(src_shift),
+                         src_from=i32(src_from), src_nbits=i32(src_nbits),
                          out_off=torch.tensor(off[:-1], dtype=torch.int64, device=dev),
-                         out_cap=i32(caps), group_desc=i32(desc),
-                         group_item_off=i32(np.concatenate([[0], np.cumsum(nits)])[:-1]))
-        self.acc = torch.empty((max(self.n_groups, 1), row_extent), dtype=torch.int32, device=dev)
-        self.n_src, self.rows, self.rpi = len(src_item), row_extent, rows_per_item
+                         out_cap=i32(caps), group_desc=i32(desc), group_item_off=i32(item_off[:-1]))
+        self.acc = torch.empty((max(self.n_all_groups, 1), row_extent), dtype=torch.int32,
+                               device=dev)
+        self.n_src, self.rows, self.rpi = len(src_item), row_extent, rpi
+        # the forward list, as indices into [all merge items | the players' items]:
+        # the forward-only groups first, the shared groups they do not replace,
+        # the players' items but the folded last ones
+        self.fwd_index = self.row_table = None
+        self.fwd_n_items = 0
+        if fwd_groups:
+            replaced = set(fwd_groups)
+            idx = list(range(self.n_items, self.n_out_items))
+            for g in range(self.n_groups):
+                if g not in replaced:
+                    idx += list(range(int(item_off[g]), int(item_off[g + 1])))
+            folded = {int(item_start[b, p]) + n_it_p - 1 for b, p in taken}
+            idx += [self.n_out_items + i - self.first_player for i in range(self.first_player, n_items)
+                    if i not in folded]
+            self.fwd_index = torch.tensor(idx, dtype=torch.int64, device=dev)
+            self.fwd_n_items = len(idx)
+            self.row_table = torch.tensor(rows_tab, dtype=torch.int32, device=dev).reshape(-1, 2)
 
-    def run(self, items, kv_idx, kv_mask, blk_and, n_items: int, stream) -> torch.Tensor:
+    def run(self, items, kv_idx, kv_mask, blk_and, n_items: int, stream):
         """Merged lists into their slots; the final items (merged hub groups,
-        then the players' items of the built list)."""
-        out = torch.empty((max(self.n_items, 1), 8), dtype=torch.int32, device=items.device)
+        then the players' items of the built list) and the forward list's
+        items (None without folded rows)."""
+        out = torch.empty((max(self.n_out_items, 1), 8), dtype=torch.int32, device=items.device)
         d = self._dev
         a = _capi.HierMergeArgs(
-            n_groups=self.n_groups, n_src=self.n_src, rows=self.rows, rows_per_item=self.rpi,
+            n_groups=self.n_all_groups, n_src=self.n_src, rows=self.rows, rows_per_item=self.rpi,
             items=items.data_ptr(), kv_idx=kv_idx.data_ptr(), kv_mask=kv_mask.data_ptr(),
             blk_and=blk_and.data_ptr(), acc=self.acc.data_ptr(),
             **{k: v.data_ptr() for k, v in d.items()}, out_items=out.data_ptr())
         _capi.call("hier_merge_hub_lists", C.byref(a), stream)
-        return torch.cat([out[:self.n_items], items[self.first_player:n_items]])
+        players = items[self.first_player:n_items]
+        shared = torch.cat([out[:self.n_items], players])
+        if self.fwd_index is None:
+            return shared, None
+        return shared, torch.cat([out[:self.n_out_items], players]).index_select(0, self.fwd_index)
 
 
 def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
           tiled: bool = False, rows_per_item: int = ROWS_PER_ITEM,
-          merge_hubs: Optional[int] = None) -> BuildResult:
+          merge_hubs: Optional[int] = None, fold_tails: Optional[bool] = None) -> BuildResult:
     """Run the two device passes and return device tensors.  With
     ``merge_hubs = G >= 2`` (full-sequence topologies), the hub streams of G
     consecutive temporal blocks share one work group (``_HubMerge``).  The
-    default merges four blocks for full-sequence topologies when no
-    reference-format arrays are requested (those callers may launch subsets
-    of blocks through ``item_ranges``, which a merged list does not keep)."""
+    default merges ``MERGE_HUB_BLOCKS`` blocks for full-sequence topologies
+    when no reference-format arrays are requested (those callers may launch
+    subsets of blocks through ``item_ranges``, which a merged list does not
+    keep).  ``fold_tails`` (default: with a merge) also writes the forward's
+    own list, in which the players' ragged last items join their local hubs'
+    groups (``TileList.fwd_items``)."""
     if merge_hubs is None:
         merge_hubs = MERGE_HUB_BLOCKS if (topo.frames_valid and not tiled and
                                           segmented_block_m is None) else 0
@@ -574,7 +690,8 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     G = min(int(merge_hubs), 32 // n) if merge_hubs else 0
     if G >= 2 and topo.frames_valid and B >= 2:
         merge = _HubMerge(topo, G, tile_h, tile_off, item_start, n_keys, n_items, rows_per_item,
-                          group_rows_cover(topo)[0], dev)
+                          group_rows_cover(topo)[0], dev,
+                          fold_tails=True if fold_tails is None else bool(fold_tails))
     cap = merge.capacity if merge is not None else n_keys
     kv_idx = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
     kv_mask = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
@@ -663,14 +780,15 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
                 key_ext = max(key_ext, max(flat) + w)
     row_ext, exact = group_rows_cover(topo)
     if merge is not None:
-        final = merge.run(items, kv_idx, kv_mask, blk_and, n_items, stream)
+        final, fwd = merge.run(items, kv_idx, kv_mask, blk_and, n_items, stream)
         n_player = n_items - merge.first_player
         tiles = TileList(items=final, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
                          n_items=int(final.shape[0]), item_ranges=(),
                          logical_pairs=int(pairs.sum()), key_extent=int(key_ext),
                          row_extent=int(row_ext), rows_per_item=rows_per_item,
                          frames_per_group=merge.frames, rows_exact_cover=exact,
-                         n_groups=merge.n_groups + P * B, merged_blocks=G)
+                         n_groups=merge.n_groups + P * B, merged_blocks=G,
+                         fwd_items=fwd, fwd_n_items=merge.fwd_n_items, row_table=merge.row_table)
         tiles._merge = merge
         tiles._prebuild_items = n_items
         assert tiles.n_items == merge.n_items + n_player
@@ -1205,7 +1323,8 @@ class MembershipLogitsPlan:
         ones = dict(membership=np.ones((T, N, P), bool), global_only=np.ones((T, P), bool))
         sup_topo = full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=window,
                                           direct=direct, no_local=no_local, **ones)
-        sup = build(sup_topo, dev).tiles
+        # no folded rows: which players' rows join which hub changes with the logits
+        sup = build(sup_topo, dev, fold_tails=False).tiles
         self.t, self._static = _topo_struct(sup_topo, dev)
         B = T // n
         fl_max = int(self.t.fl_max)
@@ -1276,7 +1395,7 @@ class MembershipLogitsPlan:
         out.tile_blk_and, out.tile_items = blk.data_ptr(), items.data_ptr()
         _capi.call("hier_meta_build", C.byref(self.t), C.byref(out), stream)
         if merge is not None:
-            items = merge.run(items, kv_idx, kv_mask, blk, n_pre, stream)
+            items, _ = merge.run(items, kv_idx, kv_mask, blk, n_pre, stream)
         tiles = TileList(items=items, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk,
                          n_items=sup.n_items, item_ranges=sup.item_ranges, logical_pairs=-1,
                          key_extent=sup.key_extent, row_extent=sup.row_extent,

@@ -344,6 +344,24 @@ static void misc_checks() {
   mb = ma; mb.la_frame = nullptr;              EXPECT(hier_membership_from_logits(&mb, nullptr), HIER_EINVAL);
   mb = ma; mb.T = INT_MAX; mb.B = INT_MAX; mb.n = 1;
   EXPECT(hier_membership_from_logits(&mb, nullptr), HIER_EINVAL);
+
+  EXPECT(hier_merge_hub_lists(nullptr, nullptr), HIER_EINVAL);
+  HierMergeArgs mg;
+  std::memset(&mg, 0, sizeof(mg));
+  mg.n_groups = 2; mg.n_src = 3; mg.rows = 1000; mg.rows_per_item = 128;
+  mg.items = dev<int32_t>(1); mg.kv_idx = dev<int32_t>(2); mg.kv_mask = dev<uint32_t>(3);
+  mg.blk_and = dev<uint32_t>(4); mg.acc = dev<uint32_t>(5); mg.src_item = dev<int32_t>(6);
+  mg.src_group = dev<int32_t>(7); mg.src_shift = dev<int32_t>(8); mg.out_off = dev<int64_t>(9);
+  mg.out_cap = dev<int32_t>(10); mg.group_desc = dev<int32_t>(11);
+  mg.group_item_off = dev<int32_t>(12); mg.out_items = dev<int32_t>(13);
+  HierMergeArgs mh = mg; mh.rows_per_item = 100;   EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
+  mh = mg; mh.rows = 0;                            EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
+  mh = mg; mh.n_groups = INT_MAX; mh.rows = INT_MAX;
+  EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
+  mh = mg; mh.acc = nullptr;                       EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
+  mh = mg; mh.src_from = dev<int32_t>(14);         EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
+  mh = mg; mh.src_nbits = dev<int32_t>(15);        EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
+  mh = mg; mh.n_groups = 0;                        EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_OK);
 }
 
 int main() {

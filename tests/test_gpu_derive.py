@@ -172,9 +172,11 @@ def test_logits_plan_equals_host_topology(case):
     for seed in (0, 1):
         lg = torch.randn(T, N, P, generator=torch.Generator().manual_seed(seed)).to(dev)
         mem = (lg > 0).cpu().numpy()
+        # the plan folds no player rows into hub groups (fold_tails=False)
         ref = M.build(M.full_sequence_topology(P=P, T=T, L=L, N=N, KL=KL, KG=KG, n=n, window=W,
                                                direct=True, membership=mem,
-                                               global_only=~mem.any(1)), dev).tiles
+                                               global_only=~mem.any(1)), dev,
+                      fold_tails=False).tiles
         got = plan.build(lg)
         torch.cuda.synchronize()
         _same_groups(got, ref, f"forward lists seed {seed}")

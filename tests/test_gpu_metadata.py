@@ -214,3 +214,82 @@ def test_merged_hub_groups_keep_every_key_set(cfg):
     for qb, qs, ql, r0, rc, off, cnt, nf in hub:
         live = idx_m[off:off + cnt][msk_m[off:off + cnt] != 0]
         assert (np.diff(live) > 0).all()
+
+
+def _fwd_row_owner(tiles):
+    """{token: (mask bit, item)} over the forward's own items, row-table
+    items (qstride -1) included."""
+    it = tiles.fwd_items[:tiles.fwd_n_items].cpu().numpy()
+    tab = tiles.row_table.cpu().numpy()
+    owner = {}
+    for k, (qb, qs, ql, r0, rc, off, cnt, nf) in enumerate(it):
+        for r in range(r0, r0 + rc):
+            if qs < 0:
+                tok, j = (int(x) for x in tab[qb + r])
+            else:
+                j, i = divmod(r, ql)
+                tok = qb + j * qs + i
+            assert tok not in owner, tok
+            owner[tok] = (j, k)
+    return owner, it
+
+
+@pytest.mark.parametrize("cfg", ["c2", "p6", "c3", "p10"])
+def test_folded_forward_list_keeps_every_key_set(cfg):
+    """The forward's own list, in which each player's ragged last item
+    (n * L mod 128 rows) joins its local hub's group under mask bits of its
+    own: every row owned once, every folded row's key set and every sampled
+    row's key set equal to the per-block list's; the hubs' key lists do not
+    grow (a member's keys are a subset of its hub's); fewer items of <= 32
+    rows; the backward's list unchanged."""
+    need_gpu()
+    import dataclasses
+    from tests.test_gpu_fullsize import _case, _rows
+    say("folded forward list", cfg)
+    meta, topo, _ = _case(cfg)
+    tiles = M.build(meta, "cuda").tiles
+    unfolded = M.build(meta, "cuda", fold_tails=False).tiles
+    plain = M.build(meta, "cuda", merge_hubs=0).tiles
+    assert tiles.fwd_items is not None and unfolded.fwd_items is None
+    assert torch.equal(tiles.items[:tiles.n_items], unfolded.items[:unfolded.n_items])
+    own_f, it_f = _fwd_row_owner(tiles)
+    own_p, it_p = _row_owner(plain)
+    assert sorted(own_f) == list(range(topo.S))
+    idx_f, msk_f = tiles.kv_idx.cpu().numpy(), tiles.kv_mask.cpu().numpy().view(np.uint32)
+    idx_p, msk_p = plain.kv_idx.cpu().numpy(), plain.kv_mask.cpu().numpy().view(np.uint32)
+    table_tokens = set(tiles.row_table[:, 0].cpu().tolist())
+    folded = sorted(t for t in table_tokens if t < topo.P * topo.T * topo.L)
+    assert folded, "no player rows folded"
+    sample = set(_rows(topo, np.random.default_rng(2), n_random=128).tolist()) | set(folded)
+    for r in sorted(sample):
+        assert _keys_of(tiles, it_f, idx_f, msk_f, own_f, int(r)) == \
+            _keys_of(plain, it_p, idx_p, msk_p, own_p, int(r)), (cfg, r)
+    # folded groups walk lists no longer than the hub group they replace
+    own_u, it_u = _row_owner(unfolded)
+    hub0 = topo.P * topo.T * topo.L
+    for qb, qs, ql, r0, rc, off, cnt, nf in it_f[it_f[:, 1] < 0]:
+        hub_tok = int(tiles.row_table[qb, 0])
+        assert hub0 <= hub_tok < hub0 + topo.T * topo.N * topo.KL
+        assert cnt <= it_u[own_u[hub_tok][1], 6]
+    small = lambda it: int((it[:, 4] <= 32).sum())
+    assert small(it_f) < small(it_u)
+    players = lambda it: int(((it[:, 0] < hub0) & (it[:, 1] >= 0)).sum())
+    assert players(it_f) == players(it_u) - len(folded) // (topo.n * topo.L % 128)
+    # the forward through both lists: the same rows, bf16 rounding apart
+    S, H, D = topo.S, 2, 128
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q, k, v = ((torch.randn(S, H, D, generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+               for _ in range(3))
+    from multics_amd.kernels import hier_attention_forward
+    outs, lses = [], []
+    for t in (tiles, unfolded):
+        o = torch.full((S, H, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+        l = torch.full((H, S), float("nan"), dtype=torch.float32, device="cuda")
+        hier_attention_forward(q, k, v, t, o, lse=l)
+        outs.append(o.float())
+        lses.append(l)
+    assert not outs[0].isnan().any() and not lses[0].isnan().any()
+    assert (outs[0] - outs[1]).abs().max().item() <= 2e-3
+    fin = torch.isfinite(lses[1])
+    assert torch.equal(fin, torch.isfinite(lses[0]))
+    assert (lses[0][fin] - lses[1][fin]).abs().max().item() <= 1e-3
