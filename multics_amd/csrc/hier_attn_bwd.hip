@@ -313,6 +313,40 @@ __device__ __forceinline__ void dq_tile_ste(QCtx<D>& c, int t, Idx<D>& inext,
   __syncthreads();
 }
 
+// Tile t of an item of at most 32 rows: waves 0 and 1 hold the same rows and
+// take one 32-key block each (wave w: block w), so such an item -- a hub
+// stream's rows, a player block's ragged last item -- runs on two waves
+// instead of one; waves 2 and 3 only copy.  The two waves' dQ and STE sums
+// are added at the end.
+template <int D, int PAR, bool STE>
+__device__ __forceinline__ void dq_tile_split(QCtx<D>& c, int t, Idx<D>& inext,
+                                              const QStages& st) {
+  if (t + 1 < c.nt) {
+    copy_tile<D, kBothRead>(c.gk, c.k_ss_b, c.ck, inext, st.k[PAR ^ 1], c.wave);
+    copy_dwords(c.kv_mask + (t + 1) * kSlab, st.m[PAR ^ 1], c.lane);
+    if (STE && t + 1 >= c.t1) copy_dwords(c.kv_cls + (t + 1) * kSlab, st.c[PAR ^ 1], c.lane);
+    copy_tile<D, kBothRead>(c.gv, c.v_ss_b, c.ck, inext, st.v[PAR ^ 1], c.wave);
+    inext = load_idx<D>(c.kv_idx, min(t + 2, c.nt - 1), c.ck.idx_off);
+  }
+  if (c.active) {
+    const int kb = c.wave;
+    const char* ks = st.k[PAR];
+    const uint32_t* mk = reinterpret_cast<const uint32_t*>(st.m[PAR]);
+    f32x16 s = row_mfma<D>(c.q, ks, c.krow, kb);
+    const f32x16 dp = row_mfma<D>(c.dov, st.v[PAR], c.krow, kb);
+    p_exp(s, c.c2, c.lse2);
+    bf16x8 ds[2];
+    if (STE && t >= c.t1)
+      ds_block<true>(s, dp, c.delta, mk, reinterpret_cast<const uint32_t*>(st.c[PAR]), c.ste,
+                     c.valid, kb, c.qframe, c.lane, ds);
+    else
+      ds_block<false>(s, dp, c.delta, mk, nullptr, nullptr, false, kb, c.qframe, c.lane, ds);
+    tr_mfma<D>(c.dq, ds, ks, c.ktr, kb);
+  }
+  wait_copies();
+  __syncthreads();
+}
+
 // With STE (membership STE folded into this pass) the kernel also sums the
 // dS of each row's gated keys per class (tile_kv_class >= 0) into LDS slots
 // and writes them to ste_partial[h][row][class] for every row it owns.
@@ -339,7 +373,10 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   const int qbase = it[0], qstride = it[1], qlen = it[2], row_start = it[3], row_count = it[4];
   const int kv_off = it[5], kv_cnt = it[6];
   c.nt = kv_cnt / kSlab;
-  c.active = c.wave * 32 < row_count;
+  // items of <= 32 rows: two waves split the key blocks (dq_tile_split)
+  const bool split = row_count <= 32 && c.nt >= 2;
+  const int rrel = split ? 0 : c.wave * 32;
+  c.active = split ? c.wave < 2 : rrel < row_count;
   c.c2 = a.scale * kLog2e;
   c.gk = reinterpret_cast<const char*>(a.k + (int64_t)head * a.k_sh);
   c.gv = reinterpret_cast<const char*>(a.v + (int64_t)head * a.v_sh);
@@ -349,6 +386,8 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   c.kv_mask = a.tile_kv_mask + kv_off;
   c.kv_cls = STE ? a.tile_kv_class + kv_off : nullptr;
   c.t1 = STE ? min(max(a.tile_ste_first[item], 0), c.nt) : c.nt;
+  // STE slots per wave (a split item's two waves sum into slots of their own,
+  // added in a fixed order at the end: the sums do not depend on timing)
   c.ste = lds_ste + (STE ? c.wave * 32 + (c.lane & 31) : 0);
   c.ck.init(c.wave, c.lane);
 #pragma unroll
@@ -360,7 +399,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   }
 
   // the lane's query row
-  const int r = c.wave * 32 + (c.lane & 31);
+  const int r = rrel + (c.lane & 31);
   c.valid = r < row_count;
   const int ri = row_start + (c.valid ? r : 0);
   c.qframe = ri / qlen;
@@ -383,7 +422,8 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   const int64_t srow = (int64_t)head * a.lse_stride_h + c.qtok;
   const float lse = a.lse[srow];
   c.lse2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
-  if (c.valid && c.lane < 32) {
+  const bool owner = !split || c.wave == 0;   // the wave that writes the row's results
+  if (c.valid && c.lane < 32 && owner) {
     a.delta[srow] = c.delta;
     a.lse2[srow] = c.lse2;
   }
@@ -406,7 +446,28 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
     wait_copies();
     __syncthreads();
     int t = 0;
-    if constexpr (!STE) {
+    if (split) {
+      for (; t + 1 < nt; t += 2) {
+        dq_tile_split<D, 0, STE>(c, t, inext, st);
+        dq_tile_split<D, 1, STE>(c, t + 1, inext, st);
+      }
+      if (t < nt) dq_tile_split<D, 0, STE>(c, t, inext, st);
+      // wave 1's dQ into wave 0's, through the K stage 0 (no copy in flight:
+      // the last tile issued none and ended with a barrier)
+      float* red = reinterpret_cast<float*>(st.k[0]);
+      static_assert(Geo<D>::NDB * 16 * 64 * 4 <= Geo<D>::TILEB, "reduction buffer");
+      if (c.wave == 1)
+#pragma unroll
+        for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) red[(db * 16 + i) * 64 + c.lane] = c.dq[db][i];
+      __syncthreads();
+      if (c.wave == 0)
+#pragma unroll
+        for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) c.dq[db][i] += red[(db * 16 + i) * 64 + c.lane];
+    } else if constexpr (!STE) {
       for (; t + 1 < nt; t += 2) {
         dq_tile<D, 0, false>(c, t, inext, st);
         dq_tile<D, 1, false>(c, t + 1, inext, st);
@@ -432,15 +493,16 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
       if (t < nt) dq_tile_ste<D, 0>(c, t, inext, st);
     }
   }
-  if (c.active && c.valid)
+  if (c.active && c.valid && owner)
     store_acc<D>(a.dq + (int64_t)c.qtok * a.dq_ss + (int64_t)head * a.dq_sh, c.dq, a.scale, c.lane);
   if constexpr (STE) {
     // every tile ended with a barrier, so both lanes' adds are in the slots
-    if (c.valid && c.lane < 32) {
+    if (c.valid && c.lane < 32 && owner) {
       float* dst = a.ste_partial + (int64_t)head * a.ste_stride_h + (int64_t)c.qtok * a.ste_classes;
 #pragma unroll
       for (int cc = 0; cc < kSteClasses; ++cc)
-        if (cc < a.ste_classes) dst[cc] = c.ste[cc * kSteSlots];
+        if (cc < a.ste_classes)
+          dst[cc] = split ? c.ste[cc * kSteSlots] + c.ste[cc * kSteSlots + 32] : c.ste[cc * kSteSlots];
     }
   }
 }
@@ -513,7 +575,12 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
   const int kbase = it[0], kstride = it[1], klen = it[2], row_start = it[3], row_count = it[4];
   const int q_off = it[5], q_cnt = it[6];
   c.nt = q_cnt / kSlab;
-  c.active = c.wave * 32 < row_count;
+  // items of <= 32 key rows (a hub stream's keys, a player block's ragged
+  // last keys): wave pairs 0 and 1 hold the same rows and take one 32-query
+  // block of every tile each (run_split); pairs 2 and 3 only copy
+  const bool split = row_count <= 32 && c.nt >= 2;
+  const int rrel = split ? 0 : c.wave * 32;
+  c.active = split ? c.wave < 2 : rrel < row_count;
   c.c2 = a.scale * kLog2e;
   c.gq = reinterpret_cast<const char*>(a.q + (int64_t)head * a.q_sh);
   c.gdo = reinterpret_cast<const char*>(a.dout + (int64_t)head * a.do_sh);
@@ -531,7 +598,7 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
     c.tr[db][0] = tr_read_off<D, kBothRead>(c.lane, db, 0);
     c.tr[db][1] = tr_read_off<D, kBothRead>(c.lane, db, 1);
   }
-  const int r = c.wave * 32 + (c.lane & 31);
+  const int r = rrel + (c.lane & 31);
   c.valid = r < row_count;
   const int ri = row_start + (c.valid ? r : 0);
   c.kframe = ri / klen;
@@ -556,59 +623,63 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
       if (c.wave == 2) dma4_lane(c.delta + qtok, lds_w[sg] + 2 * Geo<D>::MBYTES);
     }
   };
-  // role A: S and P of tile t (stage sg) into pb (bf16) and the P slot of parity par
-  auto a_front = [&](int sg, int par, bf16x8 (*pb)[2]) {
+  // role A: S and P of query block qb of tile t (stage sg) into pb (bf16)
+  // and the P slot of parity par
+  auto a_block = [&](int sg, int par, int qb, bf16x8* pb) {
     const uint32_t* mk = reinterpret_cast<const uint32_t*>(lds_w[sg]);
     const float* l2 = reinterpret_cast<const float*>(lds_w[sg] + Geo<D>::MBYTES);
+    f32x16 x = row_mfma<D>(c.kt, lds_q[sg], c.row, qb);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      f32x16 x = row_mfma<D>(c.kt, lds_q[sg], c.row, qb);
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
+      const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[q0]);
+      const u32x4 lw = *reinterpret_cast<const u32x4*>(&l2[q0]);
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
+      for (int e = 0; e < 4; ++e) {
+        const int i = 4 * g4 + e;
+        x[i] = __uint_as_float(__float_as_uint(__builtin_amdgcn_exp2f(
+                                   fmaf(x[i], c.c2, -__uint_as_float(lw[e])))) &
+                               keep_mask(w[e], c.kframe));
+        pb[i >> 3][i & 7] = (__bf16)x[i];
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      f16x8 ph;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ph[e] = (_Float16)x[8 * h + e];
+      pslot[par * 1024 + qb * 512 + h * 64] = ph;
+    }
+  };
+  auto a_front = [&](int sg, int par, bf16x8 (*pb)[2]) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) a_block(sg, par, qb, pb[qb]);
+  };
+  // role B: dS of query block qb of tile t from its P slot and dp, then
+  // dK^T += Q^T dS
+  auto b_block = [&](int sg, int par, int qb, const f32x16& dp) {
+    const float* dl = reinterpret_cast<const float*>(lds_w[sg] + 2 * Geo<D>::MBYTES);
+    bf16x8 ob[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f16x8 ph = pslot[par * 1024 + qb * 512 + h * 64];
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2) {
+        const int g4 = 2 * h + g2;
         const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
-        const u32x4 w = *reinterpret_cast<const u32x4*>(&mk[q0]);
-        const u32x4 lw = *reinterpret_cast<const u32x4*>(&l2[q0]);
+        const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * g4 + e;
-          x[i] = __uint_as_float(__float_as_uint(__builtin_amdgcn_exp2f(
-                                     fmaf(x[i], c.c2, -__uint_as_float(lw[e])))) &
-                                 keep_mask(w[e], c.kframe));
-          pb[qb][i >> 3][i & 7] = (__bf16)x[i];
+          ob[i >> 3][i & 7] = (__bf16)((float)ph[4 * g2 + e] * (dp[i] - __uint_as_float(dw[e])));
         }
       }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        f16x8 ph;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ph[e] = (_Float16)x[8 * h + e];
-        pslot[par * 1024 + qb * 512 + h * 64] = ph;
-      }
     }
+    tr_mfma<D>(c.acc, ob, lds_q[sg], c.tr, qb);   // dK^T += Q^T dS
   };
-  // role B: dS of tile t from its P slot and dp, then dK^T += Q^T dS
   auto b_back = [&](int sg, int par, const f32x16* dp) {
-    const float* dl = reinterpret_cast<const float*>(lds_w[sg] + 2 * Geo<D>::MBYTES);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      bf16x8 ob[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const f16x8 ph = pslot[par * 1024 + qb * 512 + h * 64];
-#pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-          const int g4 = 2 * h + g2;
-          const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
-          const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = 4 * g4 + e;
-            ob[i >> 3][i & 7] = (__bf16)((float)ph[4 * g2 + e] * (dp[qb][i] - __uint_as_float(dw[e])));
-          }
-        }
-      }
-      tr_mfma<D>(c.acc, ob, lds_q[sg], c.tr, qb);   // dK^T += Q^T dS
-    }
+    for (int qb = 0; qb < 2; ++qb) b_block(sg, par, qb, dp[qb]);
   };
 
   auto run = [&](auto rb) {
@@ -680,9 +751,80 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
     step(t, false);
   }
   };
-  if (role_b) run(std::true_type{});
-  else run(std::false_type{});
-  if (c.active && c.valid) {
+  // the same schedule for a split item: pair w takes query block w of every
+  // tile (its own P slot), one block of products per tile and role
+  auto run_split = [&](auto rb) {
+    constexpr bool RB = decltype(rb)::value;
+    const int nt = c.nt;
+    const int qb = c.wave;
+    const Idx<D> i0 = load_idx<D>(c.q_idx, 0, c.cq.idx_off);
+    copy_q_tile(0, i0, c.q_idx[c.lane], 0);
+    const Idx<D> i1 = load_idx<D>(c.q_idx, 1, c.cq.idx_off);   // nt >= 2
+    copy_q_tile(1, i1, c.q_idx[kSlab + c.lane], 1);
+    const int t2 = min(2, nt - 1);
+    Idx<D> inext = load_idx<D>(c.q_idx, t2, c.cq.idx_off);
+    int qnext = c.q_idx[t2 * kSlab + c.lane];
+    wait_copies();
+    __syncthreads();
+    bf16x8 pb[2];   // role A: P of block qb of the current tile
+    f32x16 dp;      // role B: dP of block qb of the current tile
+    if (c.active) {
+      if constexpr (!RB) a_block(0, 0, qb, pb);
+      else dp = row_mfma<D>(c.kt, lds_d[0], c.row, qb);
+    }
+    hier::barrier_lds();   // P of tile 0 written
+    int s0 = 0, s1 = 1, s2 = 2;
+    auto step = [&](int t, bool next) {
+      if (t + 2 < nt) {
+        copy_q_tile(t + 2, inext, qnext, s2);
+        const int t3 = min(t + 3, nt - 1);
+        inext = load_idx<D>(c.q_idx, t3, c.cq.idx_off);
+        qnext = c.q_idx[t3 * kSlab + c.lane];
+      }
+      if (c.active) {
+        if constexpr (!RB) {
+          bf16x8 pn[2];
+          if (next) a_block(s1, (t + 1) & 1, qb, pn);
+          tr_mfma<D>(c.acc, pb, lds_d[s0], c.tr, qb);   // dV^T += dO^T P
+          if (next) { pb[0] = pn[0]; pb[1] = pn[1]; }
+        } else {
+          f32x16 dn;
+          if (next) dn = row_mfma<D>(c.kt, lds_d[s1], c.row, qb);
+          b_block(s0, t & 1, qb, dp);
+          if (next) dp = dn;
+        }
+      }
+      wait_copies();
+      __syncthreads();
+      const int sx = s0; s0 = s1; s1 = s2; s2 = sx;
+    };
+    int t = 0;
+    for (; t + 1 < nt; ++t) step(t, true);
+    step(t, false);
+    // pair 1's sums into pair 0's, through the Q stages (no copy in flight:
+    // the last steps issued none and ended with a barrier)
+    float* red = reinterpret_cast<float*>(lds_q[RB ? 1 : 0]);
+    static_assert(Geo<D>::NDB * 16 * 64 * 4 <= Geo<D>::TILEB, "reduction buffer");
+    if (c.wave == 1)
+#pragma unroll
+      for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[(db * 16 + i) * 64 + c.lane] = c.acc[db][i];
+    __syncthreads();
+    if (c.wave == 0)
+#pragma unroll
+      for (int db = 0; db < Geo<D>::NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c.acc[db][i] += red[(db * 16 + i) * 64 + c.lane];
+  };
+  if (split) {
+    if (role_b) run_split(std::true_type{});
+    else run_split(std::false_type{});
+  } else {
+    if (role_b) run(std::true_type{});
+    else run(std::false_type{});
+  }
+  if (c.active && c.valid && (!split || c.wave == 0)) {
     if (role_b)
       store_acc<D>(a.dk + (int64_t)c.ktok * a.dk_ss + (int64_t)head * a.dk_sh, c.acc, a.scale, c.lane);
     else

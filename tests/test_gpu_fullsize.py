@@ -162,6 +162,12 @@ def test_backward_full_size_sampled_rows():
     H = 2
     say("full-size backward c5 S", topo.S)
     tiles = M.build(meta, "cuda").tiles
+    # items of <= 32 rows with at least two tiles: the dQ and dK/dV passes
+    # split them over two waves / wave pairs (player blocks' ragged last rows
+    # and keys, hub streams), and the sampled rows hold such rows
+    it = tiles.items[:tiles.n_items].cpu().numpy()
+    split = (it[:, 4] <= 32) & (it[:, 6] >= 128)
+    assert split.sum() >= 20
     q, k, v = _inputs(topo.S, H, D, seed=23)
     dout = torch.randn(topo.S, H, D, generator=torch.Generator().manual_seed(24)).to(torch.bfloat16)
     qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
