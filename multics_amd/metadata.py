@@ -472,8 +472,13 @@ def _member(topo: BlockTopology, b: int, f: int, g: int, p: int) -> bool:
 
 
 class _HubMerge:
-    """The hub-stream merge of a full-sequence tile list (``hier_merge_hub_lists``):
-    host plan and device arrays, replayable on new lists of the same layout.
+    """The hub-stream merge of a tile list (``hier_merge_hub_lists``): host
+    plan and device arrays, replayable on new lists of the same layout.
+
+    With ``G >= 2`` (full-sequence lists) the hub streams of G consecutive
+    temporal blocks share one group, and the shared list (forward and
+    backward) is those groups' items followed by the players' items.  With
+    ``G == 1`` nothing is merged: the shared list is the built list.
 
     With ``fold_tails`` the merge also writes a forward-only list: each local
     hub group may take the ragged last item of the players that belong to its
@@ -483,13 +488,14 @@ class _HubMerge:
     bits of their own above the hub's frames and are addressed through a row
     table of (token, bit) pairs.  The backward keeps the list without them."""
 
-    def __init__(self, topo: BlockTopology, G: int, tile_h, tile_off, item_start, n_keys: int,
-                 n_items: int, rows_per_item: int, row_extent: int, dev, fold_tails: bool = False):
+    def __init__(self, topo: BlockTopology, G: int, tile_h, item_start, nit, n_keys: int,
+                 n_items: int, rows_per_item: int, key_rows: int, dev, fold_tails: bool = False):
         P, N, n, B = topo.P, topo.N, topo.n_frames, topo.B
         rpi = rows_per_item
+        self.merge = G >= 2
         hubs = ([] if topo.no_local else list(range(P, P + N))) + [P + N]
         src_item, src_group, src_shift, src_from, src_nbits = [], [], [], [], []
-        caps, desc, nits, group_srcs = [], [], [], []
+        caps, desc, nits = [], [], []
 
         def add_source(item, group, shift, first_bit=0, nbits=32):
             src_item.append(int(item))
@@ -498,28 +504,35 @@ class _HubMerge:
             src_from.append(int(first_bit))
             src_nbits.append(int(nbits))
 
-        local_groups = []            # (group, hub stream, blocks)
+        # hub groups: merged groups of the shared list, or (G == 1) the built
+        # list's own hub items, which only the fold reads
+        local_hubs = []       # (group or None, hub stream, blocks, sources, capacity, descriptor)
         for s in hubs:
             ql = _qlen(topo, s)
             if ql <= 0:
                 continue
             kind = 1 if s < P + N else 2
-            for b0 in range(0, B, G):
-                blocks = list(range(b0, min(B, b0 + G)))
-                g = len(caps)
-                for b in blocks:
-                    add_source(item_start[b, s], g, n * (b - b0))
-                caps.append(int(sum(int(tile_h[b, s]) for b in blocks)))
-                frames = n * len(blocks)
-                desc.append([int(topo.tile_qbase[b0][s]), int(topo.tile_qstride[kind]), ql, frames])
-                nits.append(-(-ql * frames // rpi))
+            for b0 in range(0, B, max(G, 1)):
+                blocks = list(range(b0, min(B, b0 + max(G, 1))))
+                srcs = [(int(item_start[b, s]), n * (b - b0)) for b in blocks]
+                cap = int(sum(int(tile_h[b, s]) for b in blocks))
+                d = [int(topo.tile_qbase[b0][s]), int(topo.tile_qstride[kind]), ql, n * len(blocks)]
+                g = None
+                if self.merge:
+                    g = len(caps)
+                    for it_, sh in srcs:
+                        add_source(it_, g, sh)
+                    caps.append(cap)
+                    desc.append(d)
+                    nits.append(-(-ql * d[3] // rpi))
                 if kind == 1:
-                    local_groups.append((g, s, blocks))
+                    local_hubs.append((g, s, blocks, srcs, cap, d))
         self.n_groups = len(caps)                     # groups of the shared list
         self.n_items = int(sum(nits))
         # ---- forward-only groups: local hubs with their members' last items
-        rows_tab, fwd_groups, taken = [], [], set()
-        if fold_tails:
+        rows_tab, folded, replaced, taken = [], [], [], set()
+        n_it_p = r0 = 0
+        if fold_tails and topo.L > 0:
             ql_p = topo.L
             rows_p = n * ql_p
             n_it_p = -(-rows_p // rpi)
@@ -527,85 +540,85 @@ class _HubMerge:
             tail_rows = rows_p - r0
             f0, f1 = r0 // ql_p, (rows_p - 1) // ql_p
             nb = f1 - f0 + 1
-            if ql_p > 0 and tail_rows < rpi:
-                for g, s, blocks in local_groups:
-                    ql, frames = desc[g][2], desc[g][3]
-                    hub_rows = ql * frames
-                    room = max(1, -(-hub_rows // rpi)) * rpi - hub_rows
-                    bits = frames
-                    tails = []
-                    for b in blocks:
-                        for p in range(P):
-                            if ((b, p) in taken or tail_rows > room or bits + nb > 32
-                                    or int(tile_h[b, p]) == 0):
-                                continue
-                            if all(_member(topo, b, f, s - P, p) for f in range(f0, f1 + 1)):
-                                tails.append((b, p, bits))
-                                taken.add((b, p))
-                                room -= tail_rows
-                                bits += nb
-                    if not tails:
-                        continue
-                    fg = len(caps)
-                    for i in range(len(src_item)):
-                        if src_group[i] == g:
-                            add_source(src_item[i], fg, src_shift[i])
-                    table_off = len(rows_tab)
-                    qb, qs = desc[g][0], desc[g][1]
-                    for r in range(hub_rows):
-                        f = r // ql
-                        rows_tab.append((qb + f * qs + r - f * ql, f))
-                    cap = caps[g]
-                    for b, p, bit in tails:
-                        add_source(item_start[b, p], fg, bit, f0, nb)
-                        cap += int(tile_h[b, p])
-                        pb, ps = int(topo.tile_qbase[b][p]), int(topo.tile_qstride[0])
-                        for r in range(r0, rows_p):
-                            f = r // ql_p
-                            rows_tab.append((pb + f * ps + r - f * ql_p, bit + f - f0))
-                    n_rows = len(rows_tab) - table_off
-                    caps.append(cap)
-                    desc.append([table_off, -1, 1, n_rows])
-                    nits.append(-(-n_rows // rpi))
-                    fwd_groups.append(g)
+            for g, s, blocks, srcs, cap, d in (local_hubs if tail_rows < rpi else []):
+                ql, frames = d[2], d[3]
+                hub_rows = ql * frames
+                room = max(1, -(-hub_rows // rpi)) * rpi - hub_rows
+                bits = frames
+                tails = []
+                for b in blocks:
+                    for p in range(P):
+                        if ((b, p) in taken or tail_rows > room or bits + nb > 32
+                                or int(tile_h[b, p]) == 0):
+                            continue
+                        if all(_member(topo, b, f, s - P, p) for f in range(f0, f1 + 1)):
+                            tails.append((b, p, bits))
+                            taken.add((b, p))
+                            room -= tail_rows
+                            bits += nb
+                if not tails:
+                    continue
+                fg = len(caps)
+                for it_, sh in srcs:
+                    add_source(it_, fg, sh)
+                table_off = len(rows_tab)
+                for r in range(hub_rows):
+                    f = r // ql
+                    rows_tab.append((d[0] + f * d[1] + r - f * ql, f))
+                for b, p, bit in tails:
+                    add_source(item_start[b, p], fg, bit, f0, nb)
+                    cap += int(tile_h[b, p])
+                    pb, ps = int(topo.tile_qbase[b][p]), int(topo.tile_qstride[0])
+                    for r in range(r0, rows_p):
+                        f = r // ql_p
+                        rows_tab.append((pb + f * ps + r - f * ql_p, bit + f - f0))
+                n_rows = len(rows_tab) - table_off
+                caps.append(cap)
+                desc.append([table_off, -1, 1, n_rows])
+                nits.append(-(-n_rows // rpi))
+                folded.append(g)
+                if not self.merge:
+                    replaced += [int(item_start[b, s]) + i for b in blocks
+                                 for i in range(int(nit[b, s]))]
         self.n_all_groups = len(caps)
         item_off = np.concatenate([[0], np.cumsum(nits)]).astype(np.int64)
         self.n_out_items = int(item_off[-1])
         off = n_keys + np.concatenate([[0], np.cumsum(caps)]).astype(np.int64)
         self.capacity = int(off[-1])
-        self.first_player = int(item_start[0, 0])
-        self.frames = n * G
+        # first built item the shared list keeps (the players' with a merge)
+        self.first_player = int(item_start[0, 0]) if self.merge else 0
+        self.frames = n * G if self.merge else n
         self.folded_tails = len(taken)
         i32 = lambda a: torch.tensor(np.asarray(a, np.int32).reshape(-1), device=dev)
         self._dev = dict(src_item=i32(src_item), src_group=i32(src_group), src_shift=i32(src_shift),
                          src_from=i32(src_from), src_nbits=i32(src_nbits),
                          out_off=torch.tensor(off[:-1], dtype=torch.int64, device=dev),
                          out_cap=i32(caps), group_desc=i32(desc), group_item_off=i32(item_off[:-1]))
-        self.acc = torch.empty((max(self.n_all_groups, 1), row_extent), dtype=torch.int32,
+        self.acc = torch.empty((max(self.n_all_groups, 1), key_rows), dtype=torch.int32,
                                device=dev)
-        self.n_src, self.rows, self.rpi = len(src_item), row_extent, rpi
-        # the forward list, as indices into [all merge items | the players' items]:
-        # the forward-only groups first, the shared groups they do not replace,
-        # the players' items but the folded last ones
+        self.n_src, self.rows, self.rpi = len(src_item), key_rows, rpi
+        # the forward list, as indices into [all merge items | the built items
+        # the shared list keeps]: the forward-only groups first, the shared
+        # groups (or hub items) they do not replace, the players' items but
+        # the folded last ones
         self.fwd_index = self.row_table = None
         self.fwd_n_items = 0
-        if fwd_groups:
-            replaced = set(fwd_groups)
+        if folded:
             idx = list(range(self.n_items, self.n_out_items))
+            done = set(folded)
             for g in range(self.n_groups):
-                if g not in replaced:
+                if g not in done:
                     idx += list(range(int(item_off[g]), int(item_off[g + 1])))
-            folded = {int(item_start[b, p]) + n_it_p - 1 for b, p in taken}
-            idx += [self.n_out_items + i - self.first_player for i in range(self.first_player, n_items)
-                    if i not in folded]
+            skip = {int(item_start[b, p]) + n_it_p - 1 for b, p in taken} | set(replaced)
+            idx += [self.n_out_items + i - self.first_player
+                    for i in range(self.first_player, n_items) if i not in skip]
             self.fwd_index = torch.tensor(idx, dtype=torch.int64, device=dev)
             self.fwd_n_items = len(idx)
             self.row_table = torch.tensor(rows_tab, dtype=torch.int32, device=dev).reshape(-1, 2)
 
     def run(self, items, kv_idx, kv_mask, blk_and, n_items: int, stream):
-        """Merged lists into their slots; the final items (merged hub groups,
-        then the players' items of the built list) and the forward list's
-        items (None without folded rows)."""
+        """Merged lists into their slots; the shared list's items and the
+        forward list's items (None without folded rows)."""
         out = torch.empty((max(self.n_out_items, 1), 8), dtype=torch.int32, device=items.device)
         d = self._dev
         a = _capi.HierMergeArgs(
@@ -614,11 +627,11 @@ class _HubMerge:
             blk_and=blk_and.data_ptr(), acc=self.acc.data_ptr(),
             **{k: v.data_ptr() for k, v in d.items()}, out_items=out.data_ptr())
         _capi.call("hier_merge_hub_lists", C.byref(a), stream)
-        players = items[self.first_player:n_items]
-        shared = torch.cat([out[:self.n_items], players])
+        kept = items[self.first_player:n_items]
+        shared = torch.cat([out[:self.n_items], kept]) if self.merge else items[:n_items]
         if self.fwd_index is None:
             return shared, None
-        return shared, torch.cat([out[:self.n_out_items], players]).index_select(0, self.fwd_index)
+        return shared, torch.cat([out[:self.n_out_items], kept]).index_select(0, self.fwd_index)
 
 
 def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = None,
@@ -630,9 +643,10 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     default merges ``MERGE_HUB_BLOCKS`` blocks for full-sequence topologies
     when no reference-format arrays are requested (those callers may launch
     subsets of blocks through ``item_ranges``, which a merged list does not
-    keep).  ``fold_tails`` (default: with a merge) also writes the forward's
-    own list, in which the players' ragged last items join their local hubs'
-    groups (``TileList.fwd_items``)."""
+    keep).  ``fold_tails`` (default: with a merge; without one it takes the
+    built list's hub items) also writes the forward's own list, in which the
+    players' ragged last items join their local hubs' groups
+    (``TileList.fwd_items``)."""
     if merge_hubs is None:
         merge_hubs = MERGE_HUB_BLOCKS if (topo.frames_valid and not tiled and
                                           segmented_block_m is None) else 0
@@ -686,12 +700,30 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
         item_start[b, s] = cursor
         cursor += int(nit[b, s])
     n_items = cursor
+    key_ext = 0
+    for b in range(B):
+        for rows_, w in ((topo.tile_agent_base[b], topo.L), (topo.tile_local_base[b], topo.KL),
+                         (topo.tile_global_base[b], topo.KG)):
+            flat = [x for r in rows_ for x in (r if isinstance(r, (list, tuple)) else [r])]
+            if flat and w > 0:
+                key_ext = max(key_ext, max(flat) + w)
     merge = None
     G = min(int(merge_hubs), 32 // n) if merge_hubs else 0
-    if G >= 2 and topo.frames_valid and B >= 2:
-        merge = _HubMerge(topo, G, tile_h, tile_off, item_start, n_keys, n_items, rows_per_item,
-                          group_rows_cover(topo)[0], dev,
-                          fold_tails=True if fold_tails is None else bool(fold_tails))
+    merging = G >= 2 and topo.frames_valid and B >= 2
+    # the fold pays on long launches (C2: -5 %); on a cached block (C4
+    # rollout: ~3 workgroups per slot) the folded groups' long lists end the
+    # launch (+5 %), so it is on by default only with the merge
+    fold = merging if fold_tails is None else bool(fold_tails)
+    if merging:
+        merge = _HubMerge(topo, G, tile_h, item_start, nit, n_keys, n_items, rows_per_item,
+                          int(key_ext), dev, fold_tails=fold)
+    elif fold and not topo.no_local:
+        # no merge: the forward's own list only (the players' last rows in
+        # their local hubs' items), when some fold
+        merge = _HubMerge(topo, 1, tile_h, item_start, nit, n_keys, n_items, rows_per_item,
+                          int(key_ext), dev, fold_tails=True)
+        if merge.fwd_index is None:
+            merge = None
     cap = merge.capacity if merge is not None else n_keys
     kv_idx = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
     kv_mask = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
@@ -771,15 +803,8 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
 
     ranges = tuple(tuple((int(item_start[b, s]), int(item_start[b, s] + nit[b, s]))
                          for s in range(NS) if nit[b, s] > 0) for b in range(B))
-    key_ext = 0
-    for b in range(B):
-        for rows_, w in ((topo.tile_agent_base[b], topo.L), (topo.tile_local_base[b], topo.KL),
-                         (topo.tile_global_base[b], topo.KG)):
-            flat = [x for r in rows_ for x in (r if isinstance(r, (list, tuple)) else [r])]
-            if flat and w > 0:
-                key_ext = max(key_ext, max(flat) + w)
     row_ext, exact = group_rows_cover(topo)
-    if merge is not None:
+    if merge is not None and merge.merge:
         final, fwd = merge.run(items, kv_idx, kv_mask, blk_and, n_items, stream)
         n_player = n_items - merge.first_player
         tiles = TileList(items=final, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
@@ -793,12 +818,17 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
         tiles._prebuild_items = n_items
         assert tiles.n_items == merge.n_items + n_player
     else:
+        fwd = None
+        if merge is not None:          # the forward's own list only
+            _, fwd = merge.run(items, kv_idx, kv_mask, blk_and, n_items, stream)
         tiles = TileList(items=items[:n_items], kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
                          n_items=n_items, item_ranges=ranges, logical_pairs=int(pairs.sum()),
                          key_extent=int(key_ext), row_extent=int(row_ext),
                          rows_per_item=rows_per_item, frames_per_group=int(n),
-                         rows_exact_cover=exact)
-    tiles._keepalive = (dv, keep)  # device inputs must outlive the async build
+                         rows_exact_cover=exact, fwd_items=fwd,
+                         fwd_n_items=merge.fwd_n_items if merge is not None else 0,
+                         row_table=merge.row_table if merge is not None else None)
+    tiles._keepalive = (dv, keep, merge)  # device inputs must outlive the async build
     tiles._layout = (tile_off[:-1].copy(), item_start.reshape(-1).copy())   # per (block, stream)
     layouts = None
     if tiled_res is not None:

@@ -293,3 +293,64 @@ def test_folded_forward_list_keeps_every_key_set(cfg):
     fin = torch.isfinite(lses[1])
     assert torch.equal(fin, torch.isfinite(lses[0]))
     assert (lses[0][fin] - lses[1][fin]).abs().max().item() <= 1e-3
+
+
+def test_folded_forward_list_cached_block():
+    """A cached rollout block (C4: ten players in random per-block groups,
+    the window in the paged pool): with no hub merge, ``fold_tails=True``
+    folds the players' last rows into the block's local hub items (off by
+    default there: on a short launch the folded groups' long lists end it).  Every
+    query row owned once; the key sets of every folded row and of sampled
+    rows equal the unfolded list's; the forward over both lists agrees to
+    bf16 rounding (the rollout tests run the folded list against the cached
+    oracle)."""
+    need_gpu()
+    import bench
+    from multics_amd.kernels import hier_attention_forward
+    from multics_amd.paged_cache import HierPagedKVCache
+    say("folded forward list, cached block")
+    P, T, L, N, KL, KG, n, W, _, D, grp = bench.CONFIGS["c4"]
+    H = 2
+    _, mem, go = bench.grouping(grp, P, T, N, np.random.default_rng(bench.SEED))
+    act = mem.any(-1)
+    cache = HierPagedKVCache(num_players=P, num_groups=N, num_patches=L, num_local_hub_tokens=KL,
+                             num_global_hub_tokens=KG, num_heads=H, head_dim=D, local_attn_size=W,
+                             num_frame_per_block=n, device="cuda")
+    S = P * n * L + n * (N * KL + KG)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q, k, v = ((torch.randn(S, H, D, generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+               for _ in range(3))
+    b = (W + n) // n
+    for bb in range(b + 1):
+        cache.append(k, v, bb * n, n, act[bb * n:bb * n + n])
+    frames, bases, lact = cache.window(b * n + n - 1)
+    topo = M.cached_topology(
+        P=P, N=N, L=L, KL=KL, KG=KG, n_frames=n, n_block=n, local_attn=W,
+        agent_frame_lists=[tuple(frames)] * P, local_frame_lists=[tuple(frames)] * N,
+        global_frame_list=tuple(frames), local_active_frames=lact, labels=None,
+        q_active=act[b * n:b * n + n].tolist(), direct_player=True, membership=mem,
+        global_only=go, tile_bases=bases)
+    tiles = M.build(topo, "cuda", fold_tails=True).tiles
+    plain = M.build(topo, "cuda").tiles
+    assert tiles.merged_blocks == 1 and tiles.item_ranges == plain.item_ranges
+    assert tiles.fwd_items is not None and plain.fwd_items is None
+    assert torch.equal(tiles.items[:tiles.n_items], plain.items[:plain.n_items])
+    own_f, it_f = _fwd_row_owner(tiles)
+    own_p, it_p = _row_owner(plain)
+    assert sorted(own_f) == sorted(own_p) == list(range(S))
+    idx_f, msk_f = tiles.kv_idx.cpu().numpy(), tiles.kv_mask.cpu().numpy().view(np.uint32)
+    idx_p, msk_p = plain.kv_idx.cpu().numpy(), plain.kv_mask.cpu().numpy().view(np.uint32)
+    folded = sorted(t for t in set(tiles.row_table[:, 0].cpu().tolist()) if t < P * n * L)
+    assert len(folded) >= 5 * (n * L % 128)
+    rng = np.random.default_rng(3)
+    sample = set(folded) | set(range(P * n * L, S)) | set(rng.choice(S, 256, replace=False).tolist())
+    for r in sorted(sample):
+        assert _keys_of(tiles, it_f, idx_f, msk_f, own_f, int(r)) == \
+            _keys_of(plain, it_p, idx_p, msk_p, own_p, int(r)), r
+    outs = []
+    for t in (tiles, plain):
+        o = torch.full((S, H, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+        hier_attention_forward(q, cache.k, cache.v, t, o)
+        outs.append(o.float())
+    assert not outs[0].isnan().any()
+    assert (outs[0] - outs[1]).abs().max().item() <= 2e-3
