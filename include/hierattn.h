@@ -413,6 +413,12 @@ typedef struct HierBwdArgs {
   /* ste_partial[h][row][c] and writes it for every row of every item.       */
   const int32_t* tile_kv_class;
   const int32_t* tile_ste_first;   /* [n_items]                                */
+  /* Key-major items whose kstride (item[1]) is -1 take their key rows from  */
+  /* this table: row r is the pair (token, key-frame bit) at                 */
+  /* key_row_table[2 * (kbase + r)], so one item can hold the keys of        */
+  /* several streams against one query list (hier_merge_hub_lists run on the */
+  /* key-major list).  NULL if no key item does.                            */
+  const int32_t* key_row_table;
 } HierBwdArgs;
 
 int hier_attn_bwd(const HierBwdArgs* args, void* stream);

@@ -87,7 +87,8 @@ class HierBwdArgs(C.Structure):
                [("n_ste_items", i32), ("ste_classes", i32)] + \
                [(n, vp) for n in ("ste_items", "ste_kv_idx", "ste_kv_mask", "ste_kv_class",
                                   "ste_partial")] + \
-               [("ste_stride_h", i64), ("tile_kv_class", vp), ("tile_ste_first", vp)]
+               [("ste_stride_h", i64), ("tile_kv_class", vp), ("tile_ste_first", vp),
+                ("key_row_table", vp)]
 
 
 class HierPageArgs(C.Structure):

@@ -601,8 +601,16 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
   const int r = rrel + (c.lane & 31);
   c.valid = r < row_count;
   const int ri = row_start + (c.valid ? r : 0);
-  c.kframe = ri / klen;
-  c.ktok = kbase + c.kframe * kstride + (ri - c.kframe * klen);
+  if (kstride < 0) {          // key rows from the row table: (token, key-frame bit) pairs
+    c.valid = c.valid && a.key_row_table != nullptr;   // no table: the item has no rows
+    const int2 tb =
+        c.valid ? reinterpret_cast<const int2*>(a.key_row_table)[kbase + ri] : int2{0, 0};
+    c.ktok = tb.x;
+    c.kframe = tb.y;
+  } else {
+    c.kframe = ri / klen;
+    c.ktok = kbase + c.kframe * kstride + (ri - c.kframe * klen);
+  }
   if (role_b)
     load_row<D>(c.kt, a.v + (int64_t)c.ktok * a.v_ss + (int64_t)head * a.v_sh, c.lane);
   else

@@ -17,7 +17,7 @@ import torch
 
 from . import _capi
 from . import metadata as M
-from .metadata import HierTiledBlockLayout, TileList, backward_lists, ste_classes
+from .metadata import HierTiledBlockLayout, TileList, backward_lists, folded_key_list, ste_classes
 
 
 def _stream(dev) -> C.c_void_p:
@@ -181,7 +181,9 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         kt = key_tiles
     else:
         kt, ste = backward_lists(tiles, ste_geometry if list_ste else None)
-        kt = key_tiles if key_tiles is not None else kt
+        # the players' last key rows in their hubs' key items, as the forward
+        # folds their query rows (when the list has that fold)
+        kt = key_tiles if key_tiles is not None else folded_key_list(tiles, kt)
     if ste_geometry is not None and not list_ste:
         cls = ste_classes(tiles, ste_geometry)
     dev = q.device
@@ -220,7 +222,8 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         tile_items=tiles.items.data_ptr(), tile_kv_idx=tiles.kv_idx.data_ptr(),
         tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr(),
         key_items=kt.items.data_ptr(), key_q_idx=kt.kv_idx.data_ptr(),
-        key_q_mask=kt.kv_mask.data_ptr(), key_blk_and=kt.blk_and.data_ptr())
+        key_q_mask=kt.kv_mask.data_ptr(), key_blk_and=kt.blk_and.data_ptr(),
+        key_row_table=None if kt.row_table is None else kt.row_table.data_ptr())
     if ste is not None:
         sl, scls = ste
         args.n_ste_items, args.ste_classes = sl.n_items, n_cls

@@ -23,6 +23,7 @@ hier_tiled_attention.py:165-179).
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 import os
 from collections import OrderedDict
 from dataclasses import dataclass, field
@@ -531,6 +532,9 @@ class _HubMerge:
         self.n_items = int(sum(nits))
         # ---- forward-only groups: local hubs with their members' last items
         rows_tab, folded, replaced, taken = [], [], [], set()
+        # per forward-only group: the hub's built items, [(tail's built item,
+        # first bit, bits, shift)], row-table offset, rows, shared group
+        fold_groups = []
         n_it_p = r0 = 0
         if fold_tails and topo.L > 0:
             ql_p = topo.L
@@ -577,6 +581,10 @@ class _HubMerge:
                 desc.append([table_off, -1, 1, n_rows])
                 nits.append(-(-n_rows // rpi))
                 folded.append(g)
+                fold_groups.append(([int(item_start[b, s]) + i for b in blocks
+                                     for i in range(int(nit[b, s]))],
+                                    [(int(item_start[b, p]) + n_it_p - 1, f0, nb, bit)
+                                     for b, p, bit in tails], table_off, n_rows, g))
                 if not self.merge:
                     replaced += [int(item_start[b, s]) + i for b in blocks
                                  for i in range(int(nit[b, s]))]
@@ -603,6 +611,19 @@ class _HubMerge:
         # the folded last ones
         self.fwd_index = self.row_table = None
         self.fwd_n_items = 0
+        # the fold in the shared list's item numbering (the key-major list's
+        # items are the shared list's): per forward-only group, the shared
+        # items it replaces, its sources (first item, first bit, bits,
+        # shift) and its row-table range
+        n_sh = lambda i: self.n_items + i - self.first_player if self.merge else i
+        self.key_fold = []
+        for hub_built, tails, t_off, n_rows, g in fold_groups:
+            hub_items = (list(range(int(item_off[g]), int(item_off[g + 1]))) if self.merge
+                         else hub_built)
+            srcs_k = [(hub_items[0], 0, 32, 0)] + [(n_sh(ti), fb, nbits, sh)
+                                                    for ti, fb, nbits, sh in tails]
+            self.key_fold.append((hub_items + [n_sh(ti) for ti, *_ in tails], srcs_k, t_off,
+                                  n_rows))
         if folded:
             idx = list(range(self.n_items, self.n_out_items))
             done = set(folded)
@@ -829,6 +850,8 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
                          fwd_n_items=merge.fwd_n_items if merge is not None else 0,
                          row_table=merge.row_table if merge is not None else None)
     tiles._keepalive = (dv, keep, merge)  # device inputs must outlive the async build
+    # the fold plan, which the key-major list can take too (folded_key_list)
+    tiles._fold = merge if merge is not None and merge.key_fold else None
     tiles._layout = (tile_off[:-1].copy(), item_start.reshape(-1).copy())   # per (block, stream)
     layouts = None
     if tiled_res is not None:
@@ -1150,6 +1173,71 @@ def _derive_device(tiles: TileList, ste_geometry):
         ste = (lst, s_cls)
     kt._keepalive = (ws, totals)
     return kt, ste
+
+
+def folded_key_list(tiles: TileList, kt: TileList) -> TileList:
+    """The key-major list the dK / dV pass runs: ``kt`` (the key-major list of
+    ``tiles``) with the players' last key rows folded into their local hubs'
+    key items, as the forward's own list folds their query rows: the same
+    groups, the same row table (token, key-frame bit), each group's list the
+    union of its sources' query lists (``hier_merge_hub_lists`` on ``kt``'s
+    arrays, one read-back of its item sizes).  ``kt`` itself when ``tiles``
+    has no fold.  Cached on ``kt``."""
+    plan = getattr(tiles, "_fold", None)
+    if plan is None or not kt.items.is_cuda:
+        return kt
+    hit = kt.__dict__.get("_folded")
+    if hit is not None:
+        return hit
+    dev = kt.items.device
+    sizes = kt.items[:kt.n_items, 6].cpu().numpy().astype(np.int64)
+    src_item, src_group, src_from, src_nbits, src_shift, caps, desc, nits = \
+        [], [], [], [], [], [], [], []
+    drop = set()
+    for g, (items, srcs, t_off, n_rows) in enumerate(plan.key_fold):
+        drop.update(items)
+        for it, fb, nb, sh in srcs:
+            src_item.append(it)
+            src_group.append(g)
+            src_from.append(fb)
+            src_nbits.append(nb)
+            src_shift.append(sh)
+        caps.append(int(sum(sizes[it] for it, *_ in srcs)))
+        desc.append([t_off, -1, 1, n_rows])
+        nits.append(-(-n_rows // kt.rows_per_item))
+    n_key = int(kt.kv_idx.numel())
+    off = n_key + np.concatenate([[0], np.cumsum(caps)]).astype(np.int64)
+    item_off = np.concatenate([[0], np.cumsum(nits)]).astype(np.int64)
+    cap = int(off[-1])
+    i32 = dict(dtype=torch.int32, device=dev)
+    kv_idx = torch.empty(cap, **i32)
+    kv_mask = torch.empty(cap, **i32)
+    blk = torch.empty(cap // TILE_KEYS, **i32)
+    kv_idx[:n_key].copy_(kt.kv_idx)
+    kv_mask[:n_key].copy_(kt.kv_mask)
+    blk[:n_key // TILE_KEYS].copy_(kt.blk_and[:n_key // TILE_KEYS])
+    out = torch.empty((max(int(item_off[-1]), 1), 8), **i32)
+    arr = lambda a: torch.tensor(np.asarray(a, np.int32), device=dev)
+    d = dict(src_item=arr(src_item), src_group=arr(src_group), src_shift=arr(src_shift),
+             src_from=arr(src_from), src_nbits=arr(src_nbits),
+             out_off=torch.tensor(off[:-1], dtype=torch.int64, device=dev), out_cap=arr(caps),
+             group_desc=arr(desc).reshape(-1), group_item_off=arr(item_off[:-1]))
+    rows = int(kt.key_extent)                      # query rows: the lists' entries
+    acc = torch.empty((len(caps), rows), **i32)
+    a = _capi.HierMergeArgs(
+        n_groups=len(caps), n_src=len(src_item), rows=rows, rows_per_item=kt.rows_per_item,
+        items=kt.items.data_ptr(), kv_idx=kv_idx.data_ptr(), kv_mask=kv_mask.data_ptr(),
+        blk_and=blk.data_ptr(), acc=acc.data_ptr(), **{k: v.data_ptr() for k, v in d.items()},
+        out_items=out.data_ptr())
+    _capi.call("hier_merge_hub_lists", C.byref(a), torch.cuda.current_stream(dev).cuda_stream)
+    keep = torch.tensor([i for i in range(kt.n_items) if i not in drop], dtype=torch.int64,
+                        device=dev)
+    items = torch.cat([out[:int(item_off[-1])], kt.items[:kt.n_items].index_select(0, keep)])
+    folded = dataclasses.replace(kt, items=items, n_items=int(items.shape[0]), kv_idx=kv_idx,
+                                 kv_mask=kv_mask, blk_and=blk, row_table=tiles.row_table)
+    folded._keepalive = (acc, d)
+    kt.__dict__["_folded"] = folded
+    return folded
 
 
 def backward_lists(tiles: TileList, ste_geometry=None):

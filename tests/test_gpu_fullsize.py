@@ -139,21 +139,30 @@ def test_forward_c2_as_benchmarked():
 
 
 def _check_key_sets(tiles, rows, m, dead):
-    items = tiles.items[:tiles.n_items].cpu().numpy()
+    """The key set of every sampled row equals its mask row, in the shared
+    list and in the forward's own list (rows of row-table items included)."""
     idx = tiles.kv_idx.cpu().numpy()
     msk = tiles.kv_mask.cpu().numpy().view(np.uint32)
     pos = {int(r): i for i, r in enumerate(rows)}
-    seen = np.zeros(len(rows), dtype=np.int64)
-    for qbase, qstride, qlen, r0, rc, off, cnt, _ in items:
-        j, i = np.divmod(np.arange(r0, r0 + rc), qlen)
-        qs = qbase + j * qstride + i
-        for jj, qq in zip(j[np.isin(qs, rows)], qs[np.isin(qs, rows)]):
-            k = pos[int(qq)]
-            seen[k] += 1
-            got = set(idx[off:off + cnt][((msk[off:off + cnt] >> jj) & 1) == 1].tolist())
-            exp = set() if dead[k] else set(np.nonzero(m[k])[0].tolist())
-            assert got == exp, int(qq)
-    assert (seen == 1).all()
+    lists = [(tiles.items[:tiles.n_items].cpu().numpy(), None)]
+    if tiles.fwd_items is not None:
+        lists.append((tiles.fwd_items[:tiles.fwd_n_items].cpu().numpy(),
+                      tiles.row_table.cpu().numpy()))
+    for items, table in lists:
+        seen = np.zeros(len(rows), dtype=np.int64)
+        for qbase, qstride, qlen, r0, rc, off, cnt, _ in items:
+            if qstride < 0:
+                qs, j = table[qbase + r0:qbase + r0 + rc].T
+            else:
+                j, i = np.divmod(np.arange(r0, r0 + rc), qlen)
+                qs = qbase + j * qstride + i
+            for jj, qq in zip(j[np.isin(qs, rows)], qs[np.isin(qs, rows)]):
+                k = pos[int(qq)]
+                seen[k] += 1
+                got = set(idx[off:off + cnt][((msk[off:off + cnt] >> jj) & 1) == 1].tolist())
+                exp = set() if dead[k] else set(np.nonzero(m[k])[0].tolist())
+                assert got == exp, int(qq)
+        assert (seen == 1).all()
 
 
 def test_backward_full_size_sampled_rows():

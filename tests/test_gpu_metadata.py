@@ -5,6 +5,8 @@ layouts, plus the attention tile list's per-row key sets against the golden
 segmented lists and the dense-mask oracle.
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -354,3 +356,36 @@ def test_folded_forward_list_cached_block():
         outs.append(o.float())
     assert not outs[0].isnan().any()
     assert (outs[0] - outs[1]).abs().max().item() <= 2e-3
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c5"])
+def test_folded_key_major_list_keeps_every_query_set(cfg):
+    """The key-major list the dK / dV pass runs (``folded_key_list``): the
+    players' last key rows folded into their local hubs' key items under the
+    forward fold's row table.  Every key row owned once; the query set of
+    every folded key row and of sampled key rows equal to the derived
+    key-major list's; fewer items of <= 32 rows."""
+    need_gpu()
+    from tests.test_gpu_fullsize import _case, _rows
+    say("folded key-major list", cfg)
+    meta, topo, _ = _case(cfg)
+    tiles = M.build(meta, "cuda").tiles
+    kt, _ = M.backward_lists(tiles)
+    ktf = M.folded_key_list(tiles, kt)
+    assert ktf is not kt and M.folded_key_list(tiles, kt) is ktf
+    from multics_amd.kernels import _covers_all_rows
+    assert ktf.row_table is tiles.row_table and _covers_all_rows(ktf) and _covers_all_rows(kt)
+    t = dataclasses.replace(ktf, fwd_items=ktf.items, fwd_n_items=ktf.n_items)
+    own_f, it_f = _fwd_row_owner(t)
+    own_p, it_p = _row_owner(kt)
+    assert sorted(own_f) == sorted(own_p) == list(range(topo.S))
+    idx_f, msk_f = ktf.kv_idx.cpu().numpy(), ktf.kv_mask.cpu().numpy().view(np.uint32)
+    idx_p, msk_p = kt.kv_idx.cpu().numpy(), kt.kv_mask.cpu().numpy().view(np.uint32)
+    folded = sorted(x for x in set(tiles.row_table[:, 0].cpu().tolist())
+                    if x < topo.P * topo.T * topo.L)
+    assert folded
+    sample = set(_rows(topo, np.random.default_rng(4), n_random=128).tolist()) | set(folded)
+    for r in sorted(sample):
+        assert _keys_of(ktf, it_f, idx_f, msk_f, own_f, int(r)) == \
+            _keys_of(kt, it_p, idx_p, msk_p, own_p, int(r)), (cfg, r)
+    assert (it_f[:, 4] <= 32).sum() < (it_p[:, 4] <= 32).sum()
