@@ -487,7 +487,9 @@ class _HubMerge:
     group's key list does not grow), as long as the group's rows fit the
     items it has anyway and its masks have bits left.  Those rows get mask
     bits of their own above the hub's frames and are addressed through a row
-    table of (token, bit) pairs.  The backward keeps the list without them."""
+    table of (token, bit) pairs.  The dQ pass and the key-major derivation
+    keep the list without them; the dK / dV pass replays the fold on the
+    key-major list (``key_fold``, ``folded_key_list``)."""
 
     def __init__(self, topo: BlockTopology, G: int, tile_h, item_start, nit, n_keys: int,
                  n_items: int, rows_per_item: int, key_rows: int, dev, fold_tails: bool = False):
