@@ -279,13 +279,16 @@ class HierAttentionFunction(torch.autograd.Function):
                 logits: Optional[torch.Tensor] = None, ste_geometry: Optional[tuple] = None):
         q3 = _rows_view(q)[0]
         H = q3.shape[1]
+        # the output token-major whatever q's layout (the training prologue
+        # hands q over head-major): the o-projection reads it as [S, H*D]
+        # with no copy
         if _covers_all_rows(tiles) and q3.shape[0] == tiles.row_extent:
             # the kernel writes every row's output and LSE (0 and -inf for a
             # row that sees no key)
-            out = _uncleared(q)
+            out = _uncleared(size=tuple(q.shape), dtype=q.dtype, device=q.device)
             lse = _uncleared(size=(H, q3.shape[0]), dtype=torch.float32, device=q.device)
         else:
-            out = torch.zeros_like(q)
+            out = torch.zeros(tuple(q.shape), dtype=q.dtype, device=q.device)
             lse = torch.full((H, q3.shape[0]), float("-inf"), dtype=torch.float32, device=q.device)
         hier_attention_forward(q, k, v, tiles, out, lse=lse, scale=scale)
         if logits is not None:
