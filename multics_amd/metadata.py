@@ -47,6 +47,14 @@ TILED_M = 16            # hier_tiled_attention.py:32
 # blocks' members is mostly masked), C5 0.700 / 0.698 / 0.696
 MERGE_HUB_BLOCKS = 2
 
+# A forward's own list of at least this many items runs its longest key lists
+# first.  Same-box medians of five rounds, stream-major order against
+# longest-first: C2 (301 items) 2.129 / 2.093 ms, P6 (448) 3.206 / 3.169,
+# P10 (757) 6.999 / 6.901, but C5 (161 items, ~7 workgroups per slot at 24
+# heads) 0.650 / 0.662: a short launch keeps the stream-major order, whose
+# neighbouring items share key frames in L2.
+LPT_MIN_ITEMS = 256
+
 
 def _ceil(a: int, b: int) -> int:
     return -(-a // b)
@@ -829,6 +837,10 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     row_ext, exact = group_rows_cover(topo)
     if merge is not None and merge.merge:
         final, fwd = merge.run(items, kv_idx, kv_mask, blk_and, n_items, stream)
+        if fwd is not None and fwd.shape[0] >= LPT_MIN_ITEMS:
+            # longest key lists first (stable: the items of one list stay
+            # together, in stream-major order among equal lengths)
+            fwd = fwd.index_select(0, torch.argsort(-fwd[:, 6], stable=True))
         n_player = n_items - merge.first_player
         tiles = TileList(items=final, kv_idx=kv_idx, kv_mask=kv_mask, blk_and=blk_and,
                          n_items=int(final.shape[0]), item_ranges=(),
