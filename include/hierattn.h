@@ -226,6 +226,29 @@ typedef struct HierMergeArgs {
 
 int hier_merge_hub_lists(const HierMergeArgs* args, void* stream);
 
+/* Work items with each key list cut to the 64-entry tiles that some row of */
+/* the item can see: the new range runs from the first to the last such    */
+/* tile (kv_off advances by whole tiles, kv_cnt is capped at the old end);  */
+/* an item whose rows see no entry keeps its range.  A row's mask bit is    */
+/* its frame (row_start + r) / qlen, or the row table's bit for items with  */
+/* qstride -1 (row_table [rows][2] (token, bit), NULL if no item needs it). */
+/* The entries dropped are masked for every row of the item, so every pass  */
+/* over the cut list (forward, dQ, dK / dV) gives the same results while    */
+/* copying and multiplying fewer tiles.  items and out_items may be the     */
+/* same array.  No reference counterpart (the reference's kernels walk      */
+/* each segment's whole padded list: hier_tiled_attention.py:52-146,        */
+/* hier_segmented_attention.py:27-114).                                     */
+typedef struct HierTrimArgs {
+  int32_t n_items;
+  int32_t reserved;
+  const int32_t* items;            /* [n_items][8]                             */
+  const uint32_t* kv_mask;         /* the list's masks                         */
+  const int32_t* row_table;        /* [rows][2] or NULL                        */
+  int32_t* out_items;              /* [n_items][8]                             */
+} HierTrimArgs;
+
+int hier_trim_key_lists(const HierTrimArgs* args, void* stream);
+
 /* Membership-dependent topology arrays of a full-sequence membership        */
 /* topology from soft membership logits, in one launch: membership =        */
 /* logits > 0, global_only = in no group, and the query-frame / local-slot   */

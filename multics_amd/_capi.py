@@ -150,6 +150,11 @@ class HierMergeArgs(C.Structure):
                                   "group_item_off", "out_items", "src_from", "src_nbits")]
 
 
+class HierTrimArgs(C.Structure):
+    _fields_ = [("n_items", i32), ("reserved", i32)] + \
+               [(n, vp) for n in ("items", "kv_mask", "row_table", "out_items")]
+
+
 EXPORTS = {
     "hier_meta_count": [C.POINTER(HierTopo), C.POINTER(HierMetaCounts), vp],
     "hier_meta_build": [C.POINTER(HierTopo), C.POINTER(HierMetaOut), vp],
@@ -159,6 +164,7 @@ EXPORTS = {
     "hier_derive_ste_classes": [C.POINTER(HierDeriveArgs), vp, vp, vp],
     "hier_membership_from_logits": [C.POINTER(HierMembershipArgs), vp],
     "hier_merge_hub_lists": [C.POINTER(HierMergeArgs), vp],
+    "hier_trim_key_lists": [C.POINTER(HierTrimArgs), vp],
     "hier_qkv_prologue": [C.POINTER(HierPrologueArgs), vp],
     "hier_qk_prologue_bwd_waves": [C.POINTER(HierPrologueBwdArgs)],
     "hier_qk_prologue_bwd": [C.POINTER(HierPrologueBwdArgs), vp],

@@ -1483,3 +1483,73 @@ extern "C" int hier_merge_hub_lists(const HierMergeArgs* args, void* stream) {
   hipLaunchKernelGGL(merge_compact_kernel, dim3(a.n_groups), dim3(kMergeThreads), 0, s, a);
   return hier::check_launch("merge kernels");
 }
+
+// ---- key lists cut to the tiles their rows see ------------------------------
+//
+// One workgroup per item: the OR of its rows' mask bits, then the first and
+// last 64-entry tile holding an entry with one of those bits (each thread's
+// own minimum / maximum, then one LDS atomic per thread).  The item's words
+// are read into LDS before any is written, so the output may alias the input.
+namespace {
+
+constexpr int kTrimThreads = 256;
+
+__global__ __launch_bounds__(kTrimThreads) void trim_kernel(HierTrimArgs a) {
+  __shared__ int32_t it[8];
+  __shared__ uint32_t bits_s;
+  __shared__ int first_s, last_s;
+  const int64_t i = blockIdx.x;
+  if (threadIdx.x < 8) it[threadIdx.x] = a.items[8 * i + threadIdx.x];
+  if (threadIdx.x == 0) {
+    bits_s = 0u;
+    first_s = INT_MAX;
+    last_s = -1;
+  }
+  __syncthreads();
+  const int qbase = it[0], qstride = it[1], qlen = it[2], r0 = it[3], rc = it[4];
+  const int64_t off = it[5];
+  const int cnt = it[6];
+  uint32_t bits = 0u;
+  for (int r = threadIdx.x; r < rc; r += blockDim.x) {
+    int bit = -1;
+    if (qstride < 0) {
+      if (a.row_table != nullptr) bit = a.row_table[2 * ((int64_t)qbase + r0 + r) + 1];
+    } else if (qlen > 0) {
+      bit = (r0 + r) / qlen;
+    }
+    if (bit >= 0 && bit < 32) bits |= 1u << bit;
+  }
+  if (bits != 0u) atomicOr(&bits_s, bits);
+  __syncthreads();
+  bits = bits_s;
+  int lo = INT_MAX, hi = -1;
+  for (int e = threadIdx.x; e < cnt; e += blockDim.x)
+    if (a.kv_mask[off + e] & bits) {
+      lo = min(lo, e >> 6);
+      hi = max(hi, e >> 6);
+    }
+  if (hi >= 0) {
+    atomicMin(&first_s, lo);
+    atomicMax(&last_s, hi);
+  }
+  __syncthreads();
+  if (threadIdx.x < 8) {
+    int32_t v = it[threadIdx.x];
+    if (last_s >= 0 && threadIdx.x == 5) v = (int32_t)(off + 64 * (int64_t)first_s);
+    if (last_s >= 0 && threadIdx.x == 6) v = min(cnt - 64 * first_s, 64 * (last_s - first_s + 1));
+    a.out_items[8 * i + threadIdx.x] = v;
+  }
+}
+
+}  // namespace
+
+extern "C" int hier_trim_key_lists(const HierTrimArgs* args, void* stream) {
+  hier::clear_error();
+  HIER_REQUIRE(args != nullptr, HIER_EINVAL, "args is NULL");
+  const HierTrimArgs& a = *args;
+  HIER_REQUIRE(a.n_items >= 0, HIER_EINVAL, "invalid n_items=%d", a.n_items);
+  if (a.n_items == 0) return HIER_OK;
+  HIER_REQUIRE(a.items && a.kv_mask && a.out_items, HIER_EINVAL, "NULL pointer");
+  hipLaunchKernelGGL(trim_kernel, dim3(a.n_items), dim3(kTrimThreads), 0, (hipStream_t)stream, a);
+  return hier::check_launch("trim_kernel");
+}

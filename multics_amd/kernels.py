@@ -17,7 +17,7 @@ import torch
 
 from . import _capi
 from . import metadata as M
-from .metadata import HierTiledBlockLayout, TileList, backward_lists, folded_key_list, ste_classes
+from .metadata import HierTiledBlockLayout, TileList, backward_lists, folded_key_list
 
 
 def _stream(dev) -> C.c_void_p:
@@ -48,7 +48,8 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
     ``lse`` (optional, fp32 [H, S_q]) receives the natural-log softmax normaliser.
     Without ``item_range``, a list that carries the forward's own items
     (``TileList.fwd_items``: the players' ragged last items folded into their
-    hubs' groups) runs those.
+    hubs' groups) runs those.  The launch reads ``metadata.launch_list(tiles)``:
+    the same items with each key list cut to the tiles their rows can see.
     """
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
         if t.dtype != torch.bfloat16:
@@ -73,12 +74,13 @@ def hier_attention_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ti
     if lse is not None and (lse.dtype != torch.float32 or lse.dim() != 2 or lse.shape[0] != H
                             or lse.shape[1] < tiles.row_extent or lse.stride(1) != 1):
         raise ValueError("lse must be fp32 [H, >=rows] with unit row stride")
-    items, row_table = tiles.items, None
     first, last = item_range if item_range is not None else (0, tiles.n_items)
-    if item_range is None and tiles.fwd_items is not None:
-        items, row_table, last = tiles.fwd_items, tiles.row_table, tiles.fwd_n_items
     if last <= first:
         return out
+    run = M.launch_list(tiles)          # each key list cut to the tiles its rows see
+    items, row_table = run.items, tiles.row_table
+    if item_range is None and run.fwd_items is not None:
+        items, last = run.fwd_items, tiles.fwd_n_items
     args = _capi.HierFwdArgs(
         H=H, D=D, n_items=last - first, scale=float(scale if scale is not None else 1.0 / math.sqrt(D)),
         kv_rows=min(k3.shape[0], v3.shape[0]), reserved=0,
@@ -145,7 +147,12 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     ``no_alloc_workspace=True`` calls ``hier_attn_bwd_noalloc``, whose
     per-row workspace lives in the library's device array instead of a
     tensor allocated here (same results; 2 x H x rows <= 4M floats).
+
+    Both passes run ``metadata.launch_list`` of their lists (key lists cut
+    to the tiles their rows can see).
     """
+    # the derivations read the built list, not a launch list cut from it
+    tiles = tiles.__dict__.get("_source", tiles)
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
         if t.dtype != torch.bfloat16:
             raise NotImplementedError(f"{name} must be bf16, got {t.dtype}")
@@ -185,7 +192,7 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         # folds their query rows (when the list has that fold)
         kt = key_tiles if key_tiles is not None else folded_key_list(tiles, kt)
     if ste_geometry is not None and not list_ste:
-        cls = ste_classes(tiles, ste_geometry)
+        cls = M.launch_ste_first(tiles, ste_geometry)
     dev = q.device
     # every row the kernels own is written; a buffer needs clearing only when
     # some of its rows belongs to no work item: dQ over the forward list,
@@ -219,9 +226,9 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
         q_ss=q_ss, q_sh=q_sh, k_ss=k_ss, k_sh=k_sh, v_ss=v_ss, v_sh=v_sh, o_ss=o_ss, o_sh=o_sh,
         do_ss=do_ss, do_sh=do_sh, dq_ss=dq.stride(0), dq_sh=dq.stride(1), dk_ss=dk.stride(0),
         dk_sh=dk.stride(1), dv_ss=dv.stride(0), dv_sh=dv.stride(1), lse_stride_h=lse.stride(0),
-        tile_items=tiles.items.data_ptr(), tile_kv_idx=tiles.kv_idx.data_ptr(),
+        tile_items=M.launch_list(tiles).items.data_ptr(), tile_kv_idx=tiles.kv_idx.data_ptr(),
         tile_kv_mask=tiles.kv_mask.data_ptr(), tile_blk_and=tiles.blk_and.data_ptr(),
-        key_items=kt.items.data_ptr(), key_q_idx=kt.kv_idx.data_ptr(),
+        key_items=M.launch_list(kt).items.data_ptr(), key_q_idx=kt.kv_idx.data_ptr(),
         key_q_mask=kt.kv_mask.data_ptr(), key_blk_and=kt.blk_and.data_ptr(),
         key_row_table=None if kt.row_table is None else kt.row_table.data_ptr())
     if ste is not None:

@@ -867,6 +867,7 @@ def build(topo: BlockTopology, device, *, segmented_block_m: Optional[int] = Non
     # the fold plan, which the key-major list can take too (folded_key_list)
     tiles._fold = merge if merge is not None and merge.key_fold else None
     tiles._layout = (tile_off[:-1].copy(), item_start.reshape(-1).copy())   # per (block, stream)
+    launch_list(tiles)
     layouts = None
     if tiled_res is not None:
         layouts = [HierTiledBlockLayout(tiles=tiles, block=b, **d) for b, d in enumerate(tiled_res)]
@@ -1186,6 +1187,7 @@ def _derive_device(tiles: TileList, ste_geometry):
                        rows_per_item=tiles.rows_per_item)
         ste = (lst, s_cls)
     kt._keepalive = (ws, totals)
+    launch_list(kt)
     return kt, ste
 
 
@@ -1251,6 +1253,7 @@ def folded_key_list(tiles: TileList, kt: TileList) -> TileList:
                                  kv_mask=kv_mask, blk_and=blk, row_table=tiles.row_table)
     folded._keepalive = (acc, d)
     kt.__dict__["_folded"] = folded
+    launch_list(folded)
     return folded
 
 
@@ -1275,6 +1278,65 @@ def backward_lists(tiles: TileList, ste_geometry=None):
         res = (kt, ste)
     cache[key] = res
     return res
+
+
+def _trim_items(items: torch.Tensor, n: int, kv_mask: torch.Tensor,
+                row_table: Optional[torch.Tensor]) -> torch.Tensor:
+    """``hier_trim_key_lists`` into a new array (asynchronous, no read-back)."""
+    out = torch.empty_like(items)
+    if n < items.shape[0]:
+        out[n:].copy_(items[n:])
+    a = _capi.HierTrimArgs(n_items=n, items=items.data_ptr(), kv_mask=kv_mask.data_ptr(),
+                           row_table=None if row_table is None else row_table.data_ptr(),
+                           out_items=out.data_ptr())
+    _capi.call("hier_trim_key_lists", C.byref(a), torch.cuda.current_stream(items.device).cuda_stream)
+    return out
+
+
+def launch_list(tiles: TileList) -> TileList:
+    """The list the attention launches run: ``tiles`` with every item's key
+    list (``items`` and ``fwd_items``) cut to the 64-entry tiles that some of
+    its rows can see (``hier_trim_key_lists``).  The tiles cut away hold only
+    masked entries for every row of the item, so each pass gives the results
+    of the whole list.  Item order, rows and the kv arrays are shared with
+    ``tiles``; the derivations (``backward_lists``, ``folded_key_list``,
+    ``ste_classes``) keep reading ``tiles`` itself.  Built on the current
+    stream on first use and cached on ``tiles``; a host list is returned as
+    it is."""
+    hit = tiles.__dict__.get("_launch")
+    if hit is not None:
+        return hit
+    if not tiles.items.is_cuda:
+        return tiles
+    items = _trim_items(tiles.items, tiles.n_items, tiles.kv_mask, tiles.row_table)
+    fwd = None
+    if tiles.fwd_items is not None:
+        fwd = _trim_items(tiles.fwd_items, tiles.fwd_n_items, tiles.kv_mask, tiles.row_table)
+    run = dataclasses.replace(tiles, items=items, fwd_items=fwd)
+    run.__dict__["_launch"] = run
+    run._source = tiles
+    tiles.__dict__["_launch"] = run
+    return run
+
+
+def launch_ste_first(tiles: TileList, ste_geometry) -> tuple:
+    """``ste_classes(tiles, ...)`` for the launch list's items: the classes
+    per entry (positions unchanged) and each item's first tile holding one,
+    counted from its cut list's start (cached on the launch list)."""
+    cls, first = ste_classes(tiles, ste_geometry)
+    run = launch_list(tiles)
+    if run is tiles:
+        return cls, first
+    key = tuple(int(x) for x in ste_geometry)
+    cache = run.__dict__.setdefault("_ste_first", {})
+    hit = cache.get(key)
+    if hit is None:
+        n = tiles.n_items
+        shift = (run.items[:n, 5] - tiles.items[:n, 5]).div(TILE_KEYS, rounding_mode="floor")
+        hit = first.clone()
+        hit[:n] = (first[:n] - shift).clamp_(min=0)
+        cache[key] = hit
+    return cls, hit
 
 
 def transpose_tiles(tiles: TileList) -> TileList:
@@ -1554,6 +1616,8 @@ class MembershipLogitsPlan:
                       merged_blocks=sup.merged_blocks)
         tiles.__dict__["_derived"] = {None: (kt, None)}
         tiles._keepalive = (self, a, lg)
+        launch_list(tiles)
+        launch_list(kt)
         return tiles
 
 

@@ -362,6 +362,16 @@ static void misc_checks() {
   mh = mg; mh.src_from = dev<int32_t>(14);         EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
   mh = mg; mh.src_nbits = dev<int32_t>(15);        EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_EINVAL);
   mh = mg; mh.n_groups = 0;                        EXPECT(hier_merge_hub_lists(&mh, nullptr), HIER_OK);
+
+  EXPECT(hier_trim_key_lists(nullptr, nullptr), HIER_EINVAL);
+  HierTrimArgs tr;
+  std::memset(&tr, 0, sizeof(tr));
+  tr.n_items = 5; tr.items = dev<int32_t>(1); tr.kv_mask = dev<uint32_t>(2);
+  tr.out_items = dev<int32_t>(3);
+  HierTrimArgs ts = tr; ts.n_items = -1;            EXPECT(hier_trim_key_lists(&ts, nullptr), HIER_EINVAL);
+  ts = tr; ts.kv_mask = nullptr;                   EXPECT(hier_trim_key_lists(&ts, nullptr), HIER_EINVAL);
+  ts = tr; ts.out_items = nullptr;                 EXPECT(hier_trim_key_lists(&ts, nullptr), HIER_EINVAL);
+  ts = tr; ts.n_items = 0; ts.items = nullptr;     EXPECT(hier_trim_key_lists(&ts, nullptr), HIER_OK);
 }
 
 int main() {

@@ -28,6 +28,7 @@ STRUCTS = {
     "HierMembershipArgs": _capi.HierMembershipArgs,
     "HierPrologueBwdArgs": _capi.HierPrologueBwdArgs,
     "HierMergeArgs": _capi.HierMergeArgs,
+    "HierTrimArgs": _capi.HierTrimArgs,
 }
 
 

@@ -389,3 +389,74 @@ def test_folded_key_major_list_keeps_every_query_set(cfg):
         assert _keys_of(ktf, it_f, idx_f, msk_f, own_f, int(r)) == \
             _keys_of(kt, it_p, idx_p, msk_p, own_p, int(r)), (cfg, r)
     assert (it_f[:, 4] <= 32).sum() < (it_p[:, 4] <= 32).sum()
+
+
+def _check_cut(built, run, n, mask, table):
+    """Every item of ``run`` (``launch_list(built)``): same rows; its list a
+    whole-tile sub-range of the built one, starting and ending on a tile
+    with an entry some of its rows see, holding every such entry (items that
+    see none keep their range).  Returns the entries cut."""
+    b = built[:n].cpu().numpy().astype(np.int64)
+    r = run[:n].cpu().numpy().astype(np.int64)
+    assert np.array_equal(np.delete(b, [5, 6], 1), np.delete(r, [5, 6], 1))
+    m = mask.cpu().numpy().view(np.uint32)
+    rt = None if table is None else table.cpu().numpy().reshape(-1, 2)
+    cut = 0
+    for (qb, qs, ql, r0, rc, off, cnt, _), (*_, off2, cnt2, _) in zip(b, r):
+        rows = np.arange(r0, r0 + rc)
+        bits = rt[qb + rows, 1] if qs < 0 else rows // ql
+        want = np.bitwise_or.reduce(np.left_shift(np.uint32(1), bits.astype(np.uint32)))
+        seen = np.flatnonzero(m[off:off + cnt] & want)
+        if seen.size == 0:
+            assert (off2, cnt2) == (off, cnt)
+            continue
+        assert (off2 - off) % 64 == 0 and off <= off2 and off2 + cnt2 <= off + cnt
+        first, last = off2 - off, off2 - off + cnt2 - 1
+        assert first <= seen[0] and seen[-1] <= last
+        assert seen[0] // 64 == first // 64 and seen[-1] // 64 == last // 64
+        assert cnt2 == min(cnt - first, (last // 64 - first // 64 + 1) * 64)
+        cut += cnt - cnt2
+    return cut
+
+
+def _as_built(tl):
+    """``tl`` launched with its lists as built (no cut)."""
+    r = dataclasses.replace(tl)
+    r.__dict__["_launch"] = r
+    return r
+
+
+@pytest.mark.parametrize("cfg", ["c5", "c2"])
+def test_launch_lists_cut_to_visible_tiles(cfg):
+    """``launch_list``: the forward's own list, the shared list (dQ pass) and
+    the folded key-major list (dK / dV pass) cut to the tiles their rows see;
+    the forward and the backward over the cut lists equal those over the
+    built lists bit for bit (the tiles cut hold only masked entries)."""
+    need_gpu()
+    from tests.test_gpu_fullsize import _case, _inputs
+    from multics_amd.kernels import hier_attention_backward, hier_attention_forward
+    say("launch lists cut to visible tiles", cfg)
+    meta, topo, D = _case(cfg)
+    tiles = M.build(meta, "cuda").tiles
+    kt = M.folded_key_list(tiles, M.backward_lists(tiles)[0])
+    run, krun = M.launch_list(tiles), M.launch_list(kt)
+    assert M.launch_list(run) is run and M.launch_list(tiles) is run
+    cut = [_check_cut(tiles.items, run.items, tiles.n_items, tiles.kv_mask, None),
+           _check_cut(tiles.fwd_items, run.fwd_items, tiles.fwd_n_items, tiles.kv_mask,
+                      tiles.row_table),
+           _check_cut(kt.items, krun.items, kt.n_items, kt.kv_mask, kt.row_table)]
+    say("  entries cut (shared, forward, key-major)", cut)
+    assert min(cut) > 0
+    H = 2
+    q, k, v = (t.cuda() for t in _inputs(topo.S, H, D, seed=41))
+    dout = torch.randn(topo.S, H, D, generator=torch.Generator().manual_seed(42))
+    dout = dout.to(torch.bfloat16).cuda()
+    res = []
+    for t, kl in ((tiles, kt), (_as_built(tiles), _as_built(kt))):
+        o = torch.empty_like(q)
+        lse = torch.empty(H, topo.S, dtype=torch.float32, device="cuda")
+        hier_attention_forward(q, k, v, t, o, lse=lse)
+        grads = hier_attention_backward(q, k, v, o, dout, lse, t, key_tiles=kl)
+        res.append((o, lse) + tuple(grads))
+    for name, a, b in zip(("out", "lse", "dq", "dk", "dv"), *res):
+        assert torch.equal(a, b), name
