@@ -274,7 +274,7 @@ def bench_training(dev, steps=10, warmup=3):
         host read-back (``MembershipLogitsPlan``): membership from the
         logits, the tile-list pass, both key-major passes, the STE classes."""
         t_ = plan.build(lg)
-        M.ste_classes(t_, geo)
+        M.launch_ste_first(t_, geo)
         return t_
 
     def rebuild_host():
@@ -286,7 +286,7 @@ def bench_training(dev, steps=10, warmup=3):
                                               direct=True, membership=m, global_only=~m.any(1)),
                      dev).tiles
         M.backward_lists(t_, None)
-        M.ste_classes(t_, geo)
+        M.launch_ste_first(t_, geo)
         return t_
 
     def step_rebuild():

@@ -179,10 +179,10 @@ int hier_derive_build(const HierDeriveArgs* args, void* stream);
 /* P..KL, items, kv_idx, kv_mask of args; no workspace, no pass 1): g for a */
 /* local-hub key of group g in a player group's list, p for a key of player */
 /* p in a local-hub group's list, -1 for every other entry and for masks of */
-/* 0 -- the selection of the STE list, kept in forward-list order -- and    */
-/* item_first[i] = the first 64-entry tile of item i's list holding a class */
-/* (its tile count if none).  Inputs tile_kv_class / tile_ste_first of      */
-/* hier_attn_bwd.                                                           */
+/* 0 -- the selection of the STE list, kept in forward-list order; each    */
+/* item writes the entries of its own range -- and item_first[i] = the      */
+/* first 64-entry tile of item i's range holding a class (its tile count if */
+/* none).  Inputs tile_kv_class / tile_ste_first of hier_attn_bwd.          */
 int hier_derive_ste_classes(const HierDeriveArgs* args, int32_t* kv_class, int32_t* item_first,
                             void* stream);
 

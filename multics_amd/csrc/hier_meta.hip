@@ -928,23 +928,23 @@ __device__ __forceinline__ int ste_class(const HierDeriveArgs& a, const GroupDes
   return ste_class_at(a, d.qbase, k, m);
 }
 
-// Class of every entry of the list of item i's group, written by the group's
-// first item (row_start 0; entries outside [0, kv_len) are never written),
-// and the first 64-entry tile of the list holding a class, for every item.
+// Class of every entry of item i's list, written by every item over its own
+// range (the items of a group write the same values; a cut item covers part
+// of its group's list; entries outside [0, kv_len) are never written), and
+// the first 64-entry tile of the item's range holding a class.
 __global__ __launch_bounds__(kDeriveThreads) void derive_fwd_class_kernel(HierDeriveArgs a,
                                                                          int32_t* cls,
                                                                          int32_t* first) {
   __shared__ int s_first;
   const int32_t* it = a.items + 8 * (int64_t)blockIdx.x;
   const int64_t qbase = it[0], off = it[5], cnt = it[6];
-  const bool writer = it[3] == 0;
   if (threadIdx.x == 0) s_first = INT_MAX;
   __syncthreads();
   const int64_t lo = max(off, (int64_t)0), hi = min(off + cnt, (int64_t)a.kv_len);
   int mine = INT_MAX;   // this thread's first entry with a class (its entries ascend)
   for (int64_t e = lo + threadIdx.x; e < hi; e += blockDim.x) {
     const int c = ste_class_at(a, qbase, a.kv_idx[e], a.kv_mask[e]);
-    if (writer) cls[e] = c;
+    cls[e] = c;
     if (c >= 0 && mine == INT_MAX) mine = (int)(e - off);
   }
   if (mine != INT_MAX) atomicMin(&s_first, mine);
@@ -1523,7 +1523,19 @@ __global__ __launch_bounds__(kTrimThreads) void trim_kernel(HierTrimArgs a) {
   __syncthreads();
   bits = bits_s;
   int lo = INT_MAX, hi = -1;
-  for (int e = threadIdx.x; e < cnt; e += blockDim.x)
+  // four entries per load where the range allows (lists start on 64-entry
+  // tiles, so off is a multiple of 4 for every list this library builds)
+  const int n4 = (off & 3) == 0 ? cnt >> 2 : 0;
+  const uint4* m4 = reinterpret_cast<const uint4*>(a.kv_mask + off);
+  for (int q = threadIdx.x; q < n4; q += blockDim.x) {
+    const uint4 w = m4[q];
+    const bool any = ((w.x | w.y | w.z | w.w) & bits) != 0u;
+    if (any) {
+      lo = min(lo, q >> 4);
+      hi = max(hi, q >> 4);
+    }
+  }
+  for (int e = 4 * n4 + threadIdx.x; e < cnt; e += blockDim.x)
     if (a.kv_mask[off + e] & bits) {
       lo = min(lo, e >> 6);
       hi = max(hi, e >> 6);

@@ -1068,7 +1068,9 @@ def ste_classes_host(tiles: TileList, *, P: int, T: int, L: int, N: int, KL: int
     kv_idx = tiles.kv_idx.cpu().numpy().astype(np.int64)
     kv_mask = tiles.kv_mask.cpu().numpy().astype(np.int64) & 0xFFFFFFFF
     cls = np.full(len(kv_idx), -1, np.int64)
-    for qb, off, cnt in items[items[:, 3] == 0][:, [0, 5, 6]]:
+    # each item's own range (the items of a group share theirs; a launch
+    # list's cut items may each cover only part of it)
+    for qb, off, cnt in items[:, [0, 5, 6]]:
         lo, hi = max(int(off), 0), min(int(off + cnt), len(kv_idx))
         if qb >= g0 or hi <= lo:
             continue
@@ -1299,8 +1301,9 @@ def launch_list(tiles: TileList) -> TileList:
     its rows can see (``hier_trim_key_lists``).  The tiles cut away hold only
     masked entries for every row of the item, so each pass gives the results
     of the whole list.  Item order, rows and the kv arrays are shared with
-    ``tiles``; the derivations (``backward_lists``, ``folded_key_list``,
-    ``ste_classes``) keep reading ``tiles`` itself.  Built on the current
+    ``tiles``; the derivations (``backward_lists``, ``folded_key_list``)
+    keep reading ``tiles`` itself, the dQ pass's STE classes are built on
+    the launch list (``launch_ste_first``).  Built on the current
     stream on first use and cached on ``tiles``; a host list is returned as
     it is."""
     hit = tiles.__dict__.get("_launch")
@@ -1320,23 +1323,9 @@ def launch_list(tiles: TileList) -> TileList:
 
 
 def launch_ste_first(tiles: TileList, ste_geometry) -> tuple:
-    """``ste_classes(tiles, ...)`` for the launch list's items: the classes
-    per entry (positions unchanged) and each item's first tile holding one,
-    counted from its cut list's start (cached on the launch list)."""
-    cls, first = ste_classes(tiles, ste_geometry)
-    run = launch_list(tiles)
-    if run is tiles:
-        return cls, first
-    key = tuple(int(x) for x in ste_geometry)
-    cache = run.__dict__.setdefault("_ste_first", {})
-    hit = cache.get(key)
-    if hit is None:
-        n = tiles.n_items
-        shift = (run.items[:n, 5] - tiles.items[:n, 5]).div(TILE_KEYS, rounding_mode="floor")
-        hit = first.clone()
-        hit[:n] = (first[:n] - shift).clamp_(min=0)
-        cache[key] = hit
-    return cls, hit
+    """``ste_classes`` of the launch list (``launch_list(tiles)``): the
+    classes per entry and each cut item's first tile holding one."""
+    return ste_classes(launch_list(tiles), ste_geometry)
 
 
 def transpose_tiles(tiles: TileList) -> TileList:

@@ -447,6 +447,16 @@ def test_launch_lists_cut_to_visible_tiles(cfg):
            _check_cut(kt.items, krun.items, kt.n_items, kt.kv_mask, kt.row_table)]
     say("  entries cut (shared, forward, key-major)", cut)
     assert min(cut) > 0
+    geom = None
+    if topo.membership is not None:       # the membership-STE classes of the cut list
+        geom = (topo.P, topo.T, topo.L, topo.N, topo.KL)
+        cls, first = M.launch_ste_first(tiles, geom)
+        host = M.ste_classes_host(run, P=geom[0], T=geom[1], L=geom[2], N=geom[3], KL=geom[4])
+        sel = np.zeros(len(host), bool)
+        for off, cnt in run.items[:run.n_items, 5:7].cpu().numpy().astype(np.int64):
+            sel[off:off + cnt] = True
+        assert np.array_equal(cls.cpu().numpy()[sel], host[sel])
+        assert np.array_equal(first[:run.n_items].cpu().numpy(), M.ste_first_tiles_host(run, host))
     H = 2
     q, k, v = (t.cuda() for t in _inputs(topo.S, H, D, seed=41))
     dout = torch.randn(topo.S, H, D, generator=torch.Generator().manual_seed(42))
@@ -456,7 +466,7 @@ def test_launch_lists_cut_to_visible_tiles(cfg):
         o = torch.empty_like(q)
         lse = torch.empty(H, topo.S, dtype=torch.float32, device="cuda")
         hier_attention_forward(q, k, v, t, o, lse=lse)
-        grads = hier_attention_backward(q, k, v, o, dout, lse, t, key_tiles=kl)
+        grads = hier_attention_backward(q, k, v, o, dout, lse, t, key_tiles=kl, ste_geometry=geom)
         res.append((o, lse) + tuple(grads))
-    for name, a, b in zip(("out", "lse", "dq", "dk", "dv"), *res):
+    for name, a, b in zip(("out", "lse", "dq", "dk", "dv", "ste"), *res):
         assert torch.equal(a, b), name
