@@ -152,7 +152,7 @@ def hier_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o
     to the tiles their rows can see).
     """
     # the derivations read the built list, not a launch list cut from it
-    tiles = tiles.__dict__.get("_source", tiles)
+    tiles = M.built_list(tiles)
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
         if t.dtype != torch.bfloat16:
             raise NotImplementedError(f"{name} must be bf16, got {t.dtype}")

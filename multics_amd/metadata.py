@@ -25,6 +25,7 @@ from __future__ import annotations
 import ctypes as C
 import dataclasses
 import os
+import weakref
 from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Optional
@@ -1306,6 +1307,8 @@ def launch_list(tiles: TileList) -> TileList:
     the launch list (``launch_ste_first``).  Built on the current
     stream on first use and cached on ``tiles``; a host list is returned as
     it is."""
+    if tiles.__dict__.get("_is_launch"):
+        return tiles
     hit = tiles.__dict__.get("_launch")
     if hit is not None:
         return hit
@@ -1316,10 +1319,20 @@ def launch_list(tiles: TileList) -> TileList:
     if tiles.fwd_items is not None:
         fwd = _trim_items(tiles.fwd_items, tiles.fwd_n_items, tiles.kv_mask, tiles.row_table)
     run = dataclasses.replace(tiles, items=items, fwd_items=fwd)
-    run.__dict__["_launch"] = run
-    run._source = tiles
+    # no reference back to a strong owner: a list built every training step
+    # is freed when its last user drops it, without the cycle collector
+    run.__dict__["_is_launch"] = True
+    run.__dict__["_source"] = weakref.ref(tiles)
     tiles.__dict__["_launch"] = run
     return run
+
+
+def built_list(tiles: TileList) -> TileList:
+    """The list ``tiles`` was cut from when it is a launch list (while that
+    list is alive), else ``tiles``."""
+    ref = tiles.__dict__.get("_source")
+    src = ref() if ref is not None else None
+    return src if src is not None else tiles
 
 
 def launch_ste_first(tiles: TileList, ste_geometry) -> tuple:

@@ -422,7 +422,7 @@ def _check_cut(built, run, n, mask, table):
 def _as_built(tl):
     """``tl`` launched with its lists as built (no cut)."""
     r = dataclasses.replace(tl)
-    r.__dict__["_launch"] = r
+    r.__dict__["_is_launch"] = True
     return r
 
 
@@ -441,6 +441,7 @@ def test_launch_lists_cut_to_visible_tiles(cfg):
     kt = M.folded_key_list(tiles, M.backward_lists(tiles)[0])
     run, krun = M.launch_list(tiles), M.launch_list(kt)
     assert M.launch_list(run) is run and M.launch_list(tiles) is run
+    assert M.built_list(run) is tiles and M.built_list(tiles) is tiles
     cut = [_check_cut(tiles.items, run.items, tiles.n_items, tiles.kv_mask, None),
            _check_cut(tiles.fwd_items, run.fwd_items, tiles.fwd_n_items, tiles.kv_mask,
                       tiles.row_table),
