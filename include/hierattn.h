@@ -375,8 +375,8 @@ int hier_attn_fwd(const HierFwdArgs* args, void* stream);
 /* the Flex path the training forward differentiates through               */
 /* (attention.py:322-353, 367-434; hier_masks.py:690-719).                  */
 /* Two launches on `stream`: a query-major pass over the forward tile list   */
-/* (dQ; also writes delta = rowsum(dO * O) and lse2 = lse * log2(e) into the */
-/* caller's workspace) and a key-major pass over the transposed tile list     */
+/* (dQ; also writes -delta = -rowsum(dO * O) and lse2 = lse * log2(e) into  */
+/* the caller's workspace) and a key-major pass over the transposed list     */
 /* (dK, dV), so every gradient row is written by exactly one workgroup: no   */
 /* atomics, deterministic.  Gradient rows that no item covers are untouched; */
 /* key rows of a key item that no query sees are written as 0.             */

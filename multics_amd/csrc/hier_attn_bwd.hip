@@ -12,14 +12,15 @@
 //               dP^T = V dO^T         (V rows from LDS, dO^T in registers)
 //               dS^T = P^T (dP^T - delta)
 //               dQ^T += K^T dS^T      (K transposed out of LDS)
-//             Also writes delta and lse2 = lse * log2(e) per query row.
+//             Also writes -delta and lse2 = lse * log2(e) per query row.
 // dkv_kernel  key-major, over the transposed tile list (128 key rows per
 //             item, lists of query rows with a bitmask over key frames),
 //             eight waves: wave w and wave w+4 own the same 32 key rows (one
 //             wave cannot hold both accumulators at two waves per SIMD).
 //             Per 64-query tile:
 //               wave w:   S = Q K^T, P;  P to LDS;  dV^T += dO^T P
-//               wave w+4: dP = dO V^T;  dS = P (dP - delta);  dK^T += Q^T dS
+//               wave w+4: dP - delta = dO V^T accumulated onto -delta;
+//                         dS = P (dP - delta);  dK^T += Q^T dS
 //             (Q / dO rows from LDS, K^T / V^T in registers, Q / dO
 //             transposed out of LDS for the accumulations), with the S / dP
 //             products of tile t+1 overlapping the accumulations of tile t.
@@ -65,6 +66,16 @@ __device__ __forceinline__ f32x16 row_mfma(const bf16x8* b, const char* tile, co
   f32x16 s = mfma(*reinterpret_cast<const bf16x8*>(base + off[0]), b[0], zero);
 #pragma unroll
   for (int c = 1; c < Geo<D>::NC; ++c)
+    s = mfma(*reinterpret_cast<const bf16x8*>(base + off[c]), b[c], s);
+  return s;
+}
+
+template <int D>
+__device__ __forceinline__ f32x16 row_mfma_from(f32x16 s, const bf16x8* b, const char* tile,
+                                                const int* off, int blk) {
+  const char* base = tile + blk * 32 * Geo<D>::ROWB;
+#pragma unroll
+  for (int c = 0; c < Geo<D>::NC; ++c)
     s = mfma(*reinterpret_cast<const bf16x8*>(base + off[c]), b[c], s);
   return s;
 }
@@ -424,7 +435,7 @@ __global__ __launch_bounds__(kThreads, 2) void dq_kernel(HierBwdArgs a, int tota
   c.lse2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
   const bool owner = !split || c.wave == 0;   // the wave that writes the row's results
   if (c.valid && c.lane < 32 && owner) {
-    a.delta[srow] = c.delta;
+    a.delta[srow] = -c.delta;
     a.lse2[srow] = c.lse2;
   }
 #pragma unroll
@@ -663,24 +674,30 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) a_block(sg, par, qb, pb[qb]);
   };
-  // role B: dS of query block qb of tile t from its P slot and dp, then
-  // dK^T += Q^T dS
-  auto b_block = [&](int sg, int par, int qb, const f32x16& dp) {
+  // role B: dP - delta of query block qb of the tile in stage sg (the
+  // products accumulate onto -delta, which the workspace holds per query row)
+  auto b_dp = [&](int sg, int qb) {
     const float* dl = reinterpret_cast<const float*>(lds_w[sg] + 2 * Geo<D>::MBYTES);
+    f32x16 init;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[qb * 32 + 8 * g4 + 4 * (c.lane >> 5)]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) init[4 * g4 + e] = __uint_as_float(dw[e]);
+    }
+    return row_mfma_from<D>(init, c.kt, lds_d[sg], c.row, qb);
+  };
+  // role B: dS = P (dP - delta) of query block qb of tile t from its P slot
+  // (one fp16 x fp32 fused multiply per element), then dK^T += Q^T dS
+  auto b_block = [&](int sg, int par, int qb, const f32x16& dp) {
     bf16x8 ob[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const f16x8 ph = pslot[par * 1024 + qb * 512 + h * 64];
 #pragma unroll
-      for (int g2 = 0; g2 < 2; ++g2) {
-        const int g4 = 2 * h + g2;
-        const int q0 = qb * 32 + 8 * g4 + 4 * (c.lane >> 5);
-        const u32x4 dw = *reinterpret_cast<const u32x4*>(&dl[q0]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * g4 + e;
-          ob[i >> 3][i & 7] = (__bf16)((float)ph[4 * g2 + e] * (dp[i] - __uint_as_float(dw[e])));
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * h + e;
+        ob[i >> 3][i & 7] = (__bf16)fmaf((float)ph[e], dp[i], 0.f);
       }
     }
     tr_mfma<D>(c.acc, ob, lds_q[sg], c.tr, qb);   // dK^T += Q^T dS
@@ -712,8 +729,8 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
     if (c.active) {
       if constexpr (!RB) a_front(0, 0, pb);
       else {
-        dp[0] = row_mfma<D>(c.kt, lds_d[0], c.row, 0);
-        dp[1] = row_mfma<D>(c.kt, lds_d[0], c.row, 1);
+        dp[0] = b_dp(0, 0);
+        dp[1] = b_dp(0, 1);
       }
     }
     hier::barrier_lds();   // P of tile 0 written
@@ -743,8 +760,8 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
         } else {
           f32x16 dn[2];
           if (next) {
-            dn[0] = row_mfma<D>(c.kt, lds_d[s1], c.row, 0);
-            dn[1] = row_mfma<D>(c.kt, lds_d[s1], c.row, 1);
+            dn[0] = b_dp(s1, 0);
+            dn[1] = b_dp(s1, 1);
           }
           b_back(s0, t & 1, dp);
           if (next) { dp[0] = dn[0]; dp[1] = dn[1]; }
@@ -778,7 +795,7 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
     f32x16 dp;      // role B: dP of block qb of the current tile
     if (c.active) {
       if constexpr (!RB) a_block(0, 0, qb, pb);
-      else dp = row_mfma<D>(c.kt, lds_d[0], c.row, qb);
+      else dp = b_dp(0, qb);
     }
     hier::barrier_lds();   // P of tile 0 written
     int s0 = 0, s1 = 1, s2 = 2;
@@ -797,7 +814,7 @@ __global__ __launch_bounds__(kPairThreads, 1) void dkv_kernel(HierBwdArgs a, int
           if (next) { pb[0] = pn[0]; pb[1] = pn[1]; }
         } else {
           f32x16 dn;
-          if (next) dn = row_mfma<D>(c.kt, lds_d[s1], c.row, qb);
+          if (next) dn = b_dp(s1, qb);
           b_block(s0, t & 1, qb, dp);
           if (next) dp = dn;
         }
@@ -906,7 +923,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
     load_row<D>(q, a.q + (int64_t)qtok * a.q_ss + (int64_t)head * a.q_sh, lane);
     load_row<D>(dov, a.dout + (int64_t)qtok * a.do_ss + (int64_t)head * a.do_sh, lane);
     const int64_t srow = (int64_t)head * a.lse_stride_h + qtok;
-    const float lse2 = a.lse2[srow], delta = a.delta[srow];
+    const float lse2 = a.lse2[srow], delta = -a.delta[srow];
     const int nb = kv_cnt / 32;
     for (int j = wave; j < nb; j += kWaves) {
       const int64_t key = kv_idx[32 * j + r];
@@ -969,7 +986,7 @@ __global__ __launch_bounds__(kThreads, 2) void ste_kernel(HierBwdArgs a, int tot
   load_row<D>(q, a.q + (int64_t)qtok * a.q_ss + (int64_t)head * a.q_sh, lane);
   load_row<D>(dov, a.dout + (int64_t)qtok * a.do_ss + (int64_t)head * a.do_sh, lane);
   const int64_t srow = (int64_t)head * a.lse_stride_h + qtok;
-  const float lse2 = a.lse2[srow], delta = a.delta[srow];
+  const float lse2 = a.lse2[srow], delta = -a.delta[srow];
 
   // Tile t+1 is copied into the other stage while tile t is processed.
   auto copy = [&](int t, const Idx<D>& ix) {
