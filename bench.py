@@ -294,11 +294,21 @@ def bench_training(dev, steps=10, warmup=3):
         q.grad = k.grad = v.grad = lg.grad = None
         hier_attention(q, k, v, t_, membership_logits=lg, ste_geometry=geo).backward(dout)
 
+    t_plan = rebuild()
+
+    def step_plan():
+        """A step over the plan's lists built once: the same lists as a
+        rebuilding step (the plan folds no tails into the hubs' items),
+        without the rebuild."""
+        q.grad = k.grad = v.grad = lg.grad = None
+        hier_attention(q, k, v, t_plan, membership_logits=lg, ste_geometry=geo).backward(dout)
+
     ms_fwd = float(np.median(time_events(lambda: fwd(), steps, warmup)))
     ms_step = float(np.median(time_events(step, steps, warmup)))
     ms_meta = float(np.median(time_events(rebuild, steps, warmup)))
     ms_meta_host = float(np.median(time_events(rebuild_host, steps, warmup)))
     ms_step_rebuild = float(np.median(time_events(step_rebuild, steps, warmup)))
+    ms_step_plan = float(np.median(time_events(step_plan, steps, warmup)))
     E = tiles.logical_pairs
     flop_f, flop_b = 4.0 * H * D * E, 10.0 * H * D * E
     ms_bwd = ms_step - ms_fwd
@@ -308,15 +318,18 @@ def bench_training(dev, steps=10, warmup=3):
             "ms_metadata_rebuild": round(ms_meta, 4),
             "ms_metadata_rebuild_host": round(ms_meta_host, 4),
             "ms_fwd_bwd_with_rebuild": round(ms_step_rebuild, 4),
+            "ms_fwd_bwd_plan_lists": round(ms_step_plan, 4),
             "useful_tflops_fwd_bwd": round((flop_f + flop_b) / (ms_step * 1e-3) / 1e12, 2),
             "useful_tflops_bwd": round(flop_b / (ms_bwd * 1e-3) / 1e12, 2),
             "note": "bwd = dQ (query-major, with the membership STE sums) + dK/dV (key-major); "
                     "useful FLOP 4*H*D*E fwd, 10*H*D*E bwd; *_rebuild: every step rebuilds "
                     "the forward and key-major lists and the STE classes from the logits on "
                     "the device with no host read-back (MembershipLogitsPlan), as a step "
-                    "whose logits flipped membership must; ms_metadata_rebuild_host: the same "
-                    "lists through the host topology (membership, count and totals read "
-                    "back)"}
+                    "whose logits flipped membership must; ms_fwd_bwd_plan_lists: a step over "
+                    "those lists built once (they fold no player tails into the hubs' items, "
+                    "unlike the lists of ms_fwd_bwd), so with_rebuild - plan_lists is the "
+                    "rebuild's own cost; ms_metadata_rebuild_host: the same lists through the "
+                    "host topology (membership, count and totals read back)"}
 
 
 def bench_module_training(dev, steps=10, warmup=3):
