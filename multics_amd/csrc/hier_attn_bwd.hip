@@ -1232,18 +1232,16 @@ __global__ __launch_bounds__(256) void ste_reduce_kernel(HierSteReduceArgs a) {
   const int o = blockIdx.x;
   const int p = o % a.P, g = (o / a.P) % a.N, t = o / (a.P * a.N);
   const int64_t a0 = (int64_t)a.P * a.T * a.L;
-  const int n_pl = a.H * a.L, n_hub = a.H * a.KL;
+  // a head's terms are its L player rows (class g) then its KL hub rows
+  // (class p); thread j sums term j, j + 256, ... of every head, head by head
+  // (no divisions in the loop, consecutive threads on consecutive rows)
+  const int64_t pl0 = ((int64_t)p * a.T + t) * a.L;              // player p's rows at frame t
+  const int64_t hub0 = a0 + ((int64_t)t * a.N + g) * a.KL;        // group g's hub rows at frame t
   float s = 0.f;
-  for (int i = threadIdx.x; i < n_pl + n_hub; i += blockDim.x) {
-    if (i < n_pl) {
-      const int h = i / a.L, l = i - h * a.L;
-      const int64_t row = ((int64_t)p * a.T + t) * a.L + l;
-      s += a.partial[(int64_t)h * a.stride_h + row * a.classes + g];
-    } else {
-      const int j = i - n_pl, h = j / a.KL, k = j - h * a.KL;
-      const int64_t row = a0 + ((int64_t)t * a.N + g) * a.KL + k;
-      s += a.partial[(int64_t)h * a.stride_h + row * a.classes + p];
-    }
+  for (int j = threadIdx.x; j < a.L + a.KL; j += blockDim.x) {
+    const int64_t off = j < a.L ? (pl0 + j) * a.classes + g : (hub0 + j - a.L) * a.classes + p;
+#pragma unroll 8
+    for (int h = 0; h < a.H; ++h) s += a.partial[(int64_t)h * a.stride_h + off];
   }
   part[threadIdx.x] = s;
   __syncthreads();

@@ -1406,23 +1406,39 @@ __global__ __launch_bounds__(kMergeThreads) void merge_compact_kernel(HierMergeA
     first_s = -1;
   }
   __syncthreads();
-  for (int r0 = 0; r0 < a.rows; r0 += kMergeThreads) {
-    const int r = r0 + threadIdx.x;
-    const uint32_t m = r < a.rows ? acc[r] : 0u;
-    const uint64_t live = __ballot(m != 0);
-    if (lane == 0) wsum[wave] = __popcll(live);
+  // four consecutive rows per thread and pass, in row order: a thread's live
+  // rows follow those of the lower lanes of its wave and of the lower waves
+  constexpr int kRows = 4 * kMergeThreads;
+  for (int r0 = 0; r0 < a.rows; r0 += kRows) {
+    const int rb = r0 + 4 * threadIdx.x;
+    uint32_t m[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m[e] = rb + e < a.rows ? acc[rb + e] : 0u;
+    const int mine = (m[0] != 0) + (m[1] != 0) + (m[2] != 0) + (m[3] != 0);
+    int incl = mine;                       // inclusive prefix over the wave's lanes
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
     int before = 0, total = 0;
     for (int w = 0; w < kMergeThreads / 64; ++w) {
       before += w < wave ? wsum[w] : 0;
       total += wsum[w];
     }
-    const int pos = base_s + before + __popcll(live & ((1ull << lane) - 1));
-    if (m != 0 && pos < cap) {
-      a.kv_idx[out + pos] = r;
-      a.kv_mask[out + pos] = m;
+    int pos = base_s + before + incl - mine;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (m[e] == 0) continue;
+      if (pos < cap) {
+        a.kv_idx[out + pos] = rb + e;
+        a.kv_mask[out + pos] = m[e];
+      }
+      if (pos == 0) first_s = rb + e;
+      ++pos;
     }
-    if (m != 0 && pos == 0) first_s = r;
     __syncthreads();
     if (threadIdx.x == 0) base_s += total;
     __syncthreads();
