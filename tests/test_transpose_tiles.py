@@ -179,3 +179,11 @@ def test_group_rows_cover_full_sequence(kind):
     short.tile_qbase = [list(r) for r in short.tile_qbase]
     short.KL = 0                        # the local-hub rows (mid-sequence) uncovered
     assert not M.group_rows_cover(short)[1]
+
+
+def test_host_lists_launch_as_built():
+    """``launch_list`` cuts device lists only (the cut is a device pass); a
+    host list is its own launch list and its own built list."""
+    tiles = synth_forward_tiles(FullTopology(2, 6, 4, 1, 1, 1, 3, 4, True, labels=np.zeros((6, 2), np.int64)))
+    assert not tiles.items.is_cuda
+    assert M.launch_list(tiles) is tiles and M.built_list(tiles) is tiles
