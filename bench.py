@@ -238,7 +238,7 @@ def bench_forward_cfg(cfg, dev, steps=10, warmup=3):
                                      steps, warmup)))
     flop = 4.0 * H * D * tiles.logical_pairs
     del q, k, v, out
-    return {"players": P, "tokens": S, "ms_per_layer": round(ms, 4),
+    return {"players": P, "tokens": S, "window": W, "ms_per_layer": round(ms, 4),
             "useful_tflops": round(flop / (ms * 1e-3) / 1e12, 2),
             "frac_peak": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "grouping": grp}
@@ -646,6 +646,7 @@ def bench_action_temporal(dev, passes=20):
 
 # the suite of the default run, in its order: name -> fn(dev[, steps, warmup])
 SUITES = {
+    "fwd_c2_w7": lambda dev, *a: bench_forward_cfg("c2_w7", dev, *a),
     "fwd_p6": lambda dev, *a: bench_forward_cfg("p6", dev, *a),
     "fwd_c3": lambda dev, *a: bench_forward_cfg("c3", dev, *a),
     "fwd_p10": lambda dev, *a: bench_forward_cfg("p10", dev, *a),

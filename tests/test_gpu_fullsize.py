@@ -68,7 +68,7 @@ def _inputs(S, H, D, seed):
     return [(torch.randn(S, H, D, generator=g) * 0.5).to(torch.bfloat16) for _ in range(3)]
 
 
-@pytest.mark.parametrize("cfg", ["c2", "c3", "p10"])
+@pytest.mark.parametrize("cfg", ["c2", "c2_w7", "c3", "p10"])
 def test_forward_full_size_sampled_rows(cfg):
     need_gpu()
     meta, topo, D = _case(cfg)
