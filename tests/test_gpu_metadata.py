@@ -471,3 +471,65 @@ def test_launch_lists_cut_to_visible_tiles(cfg):
         res.append((o, lse) + tuple(grads))
     for name, a, b in zip(("out", "lse", "dq", "dk", "dv", "ste"), *res):
         assert torch.equal(a, b), name
+
+
+def _cut_host(items, mask, table):
+    """Expected cut of every item: the first and last 64-entry tile holding an
+    entry that one of its rows sees (rows' bits: frame (r0 + r) // qlen, or
+    the row table's bit); unchanged when no row sees any entry."""
+    out = items.copy()
+    for i, (qb, qs, ql, r0, rc, off, cnt, _) in enumerate(items.astype(np.int64)):
+        rows = np.arange(r0, r0 + rc)
+        bits = table[qb + rows, 1] if qs < 0 else rows // max(ql, 1)
+        want = np.uint32(0)
+        for b in np.unique(bits):
+            if 0 <= b < 32:
+                want |= np.uint32(1) << np.uint32(b)
+        seen = np.flatnonzero(mask[off:off + cnt] & want)
+        if seen.size:
+            f, l = seen[0] // 64, seen[-1] // 64
+            out[i, 5] = off + 64 * f
+            out[i, 6] = min(cnt - 64 * f, 64 * (l - f + 1))
+    return out
+
+
+def test_trim_kernel_random_lists():
+    """``hier_trim_key_lists`` on random items: ragged and empty ranges,
+    visible entries only at either end or nowhere, row-table items, ranges
+    not a multiple of four long or four-aligned."""
+    need_gpu()
+    rng = np.random.default_rng(11)
+    n_items, n_keys, n_rows = 400, 1 << 16, 4096
+    mask = np.zeros(n_keys, np.uint32)
+    table = np.stack([rng.integers(0, 1 << 20, n_rows), rng.integers(0, 8, n_rows)], 1).astype(np.int32)
+    items = np.zeros((n_items, 8), np.int32)
+    for i in range(n_items):
+        off = int(rng.integers(0, n_keys // 64 - 40)) * 64 + (int(rng.integers(1, 4)) if i % 7 == 0 else 0)
+        cnt = int(rng.integers(0, 40 * 64)) if i % 5 else int(rng.integers(0, 4)) * 64
+        cnt = min(cnt, n_keys - off)
+        rc = int(rng.integers(1, 129))
+        if i % 3 == 0:           # rows from the row table
+            qb = int(rng.integers(0, n_rows - 128))
+            items[i] = (qb, -1, 1, 0, rc, off, cnt, 1)
+        else:
+            ql = int(rng.integers(1, 300))
+            items[i] = (0, ql, ql, int(rng.integers(0, 200)), rc, off, cnt, 8)
+        kind = i % 4
+        seg = np.arange(off, off + cnt)
+        if cnt and kind == 0:      # sparse random bits
+            mask[seg] |= (rng.random(cnt) < 0.02).astype(np.uint32) << rng.integers(0, 8, cnt).astype(np.uint32)
+        elif cnt and kind == 1:    # one visible entry near the end
+            mask[off + cnt - 1 - int(rng.integers(0, min(cnt, 70)))] |= np.uint32(0xff)
+    dev = torch.device("cuda")
+    t_items = torch.from_numpy(items).to(dev)
+    t_mask = torch.from_numpy(mask.view(np.int32)).to(dev)
+    t_table = torch.from_numpy(table).to(dev)
+    got = M._trim_items(t_items, n_items, t_mask, t_table).cpu().numpy()
+    want = _cut_host(items, mask, table)
+    assert np.array_equal(got, want)
+    assert (got[:, 6] < items[:, 6]).sum() > 50
+    # in place (the output array is the input)
+    a = M._capi.HierTrimArgs(n_items=n_items, items=t_items.data_ptr(), kv_mask=t_mask.data_ptr(),
+                             row_table=t_table.data_ptr(), out_items=t_items.data_ptr())
+    M._capi.call("hier_trim_key_lists", M.C.byref(a), torch.cuda.current_stream().cuda_stream)
+    assert np.array_equal(t_items.cpu().numpy(), want)
