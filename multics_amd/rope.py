@@ -14,6 +14,7 @@ multics/models/wan_video_dit.py:338-389): per token 64 rotations in four bands
 from __future__ import annotations
 
 import os
+from collections import OrderedDict
 from typing import Tuple
 
 import torch
@@ -116,9 +117,30 @@ def build_self_attn_freqs_with_hub(freqs_bands, simplex_vertices, f, h, w, devic
     return torch.cat([agent, hub], dim=0)
 
 
+# The last tables converted: every layer of a model step receives the same
+# complex table, so the conversion runs once per step, not once per layer.
+# An entry holds its table (its storage cannot be reused while the entry
+# lives) and the table's version counter (an in-place change is a miss).
+_COS_SIN_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+_COS_SIN_CACHE_SIZE = 2
+
+
 def freqs_to_cos_sin(freqs: torch.Tensor, device=None):
-    """``[S,1,D/2]`` (or ``[S,D/2]``) complex table -> fp32 (cos, sin) ``[S,D/2]`` on ``device``."""
+    """``[S,1,D/2]`` (or ``[S,D/2]``) complex table -> fp32 (cos, sin) ``[S,D/2]`` on ``device``.
+    The result of the last tables is cached (keyed by the table object, its
+    version counter and the device)."""
+    dev = torch.device(device) if device is not None else freqs.device
+    key = (id(freqs), freqs._version, str(dev))
+    hit = _COS_SIN_CACHE.get(key)
+    if hit is not None and hit[0] is freqs:
+        _COS_SIN_CACHE.move_to_end(key)
+        return hit[1], hit[2]
     f = freqs.reshape(freqs.shape[0], -1)
     if device is not None:
         f = f.to(device)
-    return f.real.to(torch.float32).contiguous(), f.imag.to(torch.float32).contiguous()
+    cs, sn = f.real.to(torch.float32).contiguous(), f.imag.to(torch.float32).contiguous()
+    if not freqs.requires_grad:
+        _COS_SIN_CACHE[key] = (freqs, cs, sn)
+        while len(_COS_SIN_CACHE) > _COS_SIN_CACHE_SIZE:
+            _COS_SIN_CACHE.popitem(last=False)
+    return cs, sn

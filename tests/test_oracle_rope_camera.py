@@ -153,6 +153,23 @@ def test_product_freqs_match_oracle():
     assert torch.allclose(sn, want[:, 0].imag.float(), atol=1e-7)
 
 
+def test_cos_sin_of_a_table_is_converted_once():
+    """The conversion of the same table object is reused (every layer of a
+    step receives the same table); an in-place change of the table, or
+    another table object, converts again."""
+    t = torch.polar(torch.ones(6, 1, 4, dtype=torch.float64),
+                    torch.arange(24, dtype=torch.float64).reshape(6, 1, 4) / 7)
+    cs, sn = PR.freqs_to_cos_sin(t)
+    again = PR.freqs_to_cos_sin(t)
+    assert again[0] is cs and again[1] is sn
+    t.mul_(1j)                                    # rotate every entry by 90 degrees in place
+    cs2, sn2 = PR.freqs_to_cos_sin(t)
+    assert cs2 is not cs and torch.allclose(cs2, -sn) and torch.allclose(sn2, cs)
+    other = t.clone()
+    assert PR.freqs_to_cos_sin(other)[0] is not cs2
+    assert torch.equal(PR.freqs_to_cos_sin(other)[0], cs2)
+
+
 # ---- camera ------------------------------------------------------------------
 
 def _poses(P, T, seed):
